@@ -1,0 +1,382 @@
+/*
+ * Test infrastructure only (see cpu_ops.h): a C restatement of the drift
+ * runner's CPU reference backend for the fused layer kernels' path. Built with
+ * -ffp-contract=off and SSE arithmetic so each double and float operation
+ * rounds exactly where the JVM's does.
+ */
+#include "cpu_ops.h"
+
+#include <math.h>
+#include <string.h>
+
+static uint32_t float_bits(float v) {
+  uint32_t b;
+  memcpy(&b, &v, 4);
+  return b;
+}
+
+static float bits_float(uint32_t b) {
+  float v;
+  memcpy(&v, &b, 4);
+  return v;
+}
+
+/* CpuOps.toBfloat16 (ops/CpuOps.scala:426-431): round to nearest even on the
+ * bit pattern; a NaN keeps its top half with the quiet bit set. */
+uint16_t oracle_to_bf16(float value) {
+  const uint32_t bits = float_bits(value);
+  if (value != value) return (uint16_t)((bits >> 16) | 0x40u);
+  return (uint16_t)((bits + 0x7fffu + ((bits >> 16) & 1u)) >> 16);
+}
+
+/* DType.BF16.decodeElement (tensor/DType.scala:99-102): the top half of an F32. */
+float oracle_from_bf16(uint16_t bits) { return bits_float((uint32_t)bits << 16); }
+
+/* Float.float16ToFloat as LittleEndian.float16 uses it
+ * (tensor/LittleEndian.scala:147-148): exact, subnormals included; a NaN keeps
+ * its significand shifted into the float's top bits. */
+float oracle_f16_to_f32(uint16_t h) {
+  const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  const uint32_t exponent = (h >> 10) & 0x1fu;
+  const uint32_t significand = h & 0x3ffu;
+  if (exponent == 0) {
+    /* zero or subnormal: significand x 2^-24, exact in float */
+    const float magnitude = (float)significand * 0x1p-24f;
+    return sign ? -magnitude : magnitude;
+  }
+  if (exponent == 31) return bits_float(sign | 0x7f800000u | (significand << 13));
+  return bits_float(sign | ((exponent + 112u) << 23) | (significand << 13));
+}
+
+/* Float.floatToFloat16 for finite values and infinities: round to nearest
+ * even, overflow to infinity, subnormal results rounded on their own grid.
+ * A NaN becomes a quiet NaN with the float's top significand bits (its
+ * payload is not pinned against the JDK). */
+uint16_t oracle_f32_to_f16(float value) {
+  const uint32_t bits = float_bits(value);
+  const uint16_t sign = (uint16_t)((bits >> 16) & 0x8000u);
+  const uint32_t magnitude = bits & 0x7fffffffu;
+  if (magnitude > 0x7f800000u) return (uint16_t)(sign | 0x7e00u | ((magnitude >> 13) & 0x3ffu));
+  if (magnitude >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u); /* >= 65520: rounds to infinity */
+  const int exponent = (int)(magnitude >> 23) - 127;
+  if (exponent < -25) return sign; /* below half the smallest subnormal */
+  uint32_t significand = (magnitude & 0x7fffffu) | 0x800000u;
+  int shift; /* bits dropped from the 24-bit significand */
+  uint32_t biased;
+  if (exponent < -14) {
+    shift = 13 + (-14 - exponent);
+    biased = 0;
+  } else {
+    shift = 13;
+    biased = (uint32_t)(exponent + 15);
+    significand &= 0x7fffffu;
+  }
+  uint32_t kept = significand >> shift;
+  const uint32_t dropped = significand & ((1u << shift) - 1u);
+  const uint32_t half = 1u << (shift - 1);
+  if (dropped > half || (dropped == half && (kept & 1u))) kept += 1u;
+  /* a carry out of the significand moves into the exponent field */
+  return (uint16_t)(sign | ((biased << 10) + kept));
+}
+
+void oracle_f32_to_bf16_n(const float* x, uint16_t* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = oracle_to_bf16(x[i]);
+}
+
+void oracle_bf16_to_f32_n(const uint16_t* x, float* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = oracle_from_bf16(x[i]);
+}
+
+void oracle_f32_to_f16_n(const float* x, uint16_t* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = oracle_f32_to_f16(x[i]);
+}
+
+void oracle_f16_to_f32_n(const uint16_t* x, float* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = oracle_f16_to_f32(x[i]);
+}
+
+/* CpuOps.erf (ops/CpuOps.scala:400-424): odd; the Maclaurin series of erf
+ * below 2.5, summed until a term no longer moves the sum; the continued
+ * fraction of erfc, 60 levels deep, from 2.5 on. */
+double oracle_erf(double x) {
+  if (x < 0) return -oracle_erf(-x);
+  if (x < 2.5) {
+    double term = x, sum = x;
+    int n = 0;
+    while (fabs(term) > 1e-17 * fabs(sum)) {
+      n += 1;
+      term *= -x * x / n;
+      sum += term / (2 * n + 1);
+    }
+    return 2 / sqrt(M_PI) * sum;
+  }
+  double fraction = 0.0;
+  for (int n = 60; n >= 1; --n) fraction = (n / 2.0) / (x + fraction);
+  return 1 - exp(-x * x) / sqrt(M_PI) / (x + fraction);
+}
+
+/* CpuNormalisation.activate (ops/CpuNormalisation.scala:11-20); kinds as
+ * ops/Activation.scala:6-20: 0 SiLU, 1 GELU-tanh, 2 GELU-erf, 3 sigmoid,
+ * 4 SiTU. */
+double oracle_activate(int kind, double v) {
+  switch (kind) {
+    case 0:
+      return v / (1 + exp(-v));
+    case 1:
+      return 0.5 * v * (1 + tanh(sqrt(2 / M_PI) * (v + 0.044715 * v * v * v)));
+    case 2:
+      return 0.5 * v * (1 + oracle_erf(v / sqrt(2)));
+    case 3:
+      return 1 / (1 + exp(-v));
+    default:
+      return 4 * tanh(v / 4) / (1 + exp(-v));
+  }
+}
+
+/* CpuNormalisation.gatedUp (ops/CpuNormalisation.scala:22-24) */
+static double gated_up(int kind, double v) { return kind == 4 ? 25 * tanh(v / 25) : v; }
+
+/* CpuNormalisation.scaledActivation (ops/CpuNormalisation.scala:26-35): the
+ * input scale, a float, multiplies the value in double. */
+void oracle_activation(int kind, float input_scale, const float* x, float* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = (float)oracle_activate(kind, (double)input_scale * (double)x[i]);
+}
+
+/* CpuNormalisation.gated (ops/CpuNormalisation.scala:37-41) */
+void oracle_gated(int kind, const float* gate, const float* up, float* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i)
+    out[i] = (float)(oracle_activate(kind, (double)gate[i]) * gated_up(kind, (double)up[i]));
+}
+
+/* Ops.addRmsNorm's two steps (ops/NormalisationOps.scala:135-138): add
+ * (ops/CpuElementwise.scala:188-192), then CpuNormalisation.rmsNorm
+ * (ops/CpuNormalisation.scala:53-71): the squares summed in double, the factor
+ * 1/sqrt(mean + eps) in double, each value x * factor * (w + offset) in
+ * double, rounded to float. */
+void oracle_rms_norm(float* x, const float* y, const float* weight, float* out, int64_t rows, int64_t cols,
+                     float eps, float offset, int64_t weight_rows) {
+  for (int64_t r = 0; r < rows; ++r) {
+    float* row = x + r * cols;
+    if (y)
+      for (int64_t c = 0; c < cols; ++c) row[c] = (float)((double)row[c] + (double)y[r * cols + c]);
+    double squares = 0.0;
+    for (int64_t c = 0; c < cols; ++c) squares += (double)row[c] * (double)row[c];
+    const double factor = 1 / sqrt(squares / (double)cols + (double)eps);
+    const float* w = weight + (r % weight_rows) * cols;
+    for (int64_t c = 0; c < cols; ++c)
+      out[r * cols + c] = (float)((double)row[c] * factor * ((double)w[c] + (double)offset));
+  }
+}
+
+/* CpuNormalisation.layerNorm (ops/CpuNormalisation.scala:128-151): mean, then
+ * the variance about it (two passes, double), factor 1/sqrt(var + eps);
+ * value = normal * (w or 1) + (b or 0). */
+void oracle_layer_norm(const float* x, const float* weight, const float* bias, float* out, int64_t rows,
+                       int64_t cols, float eps) {
+  for (int64_t r = 0; r < rows; ++r) {
+    const float* row = x + r * cols;
+    double sum = 0.0;
+    for (int64_t c = 0; c < cols; ++c) sum += (double)row[c];
+    const double mean = sum / (double)cols;
+    double squares = 0.0;
+    for (int64_t c = 0; c < cols; ++c) {
+      const double d = (double)row[c] - mean;
+      squares += d * d;
+    }
+    const double variance = squares / (double)cols;
+    const double factor = 1 / sqrt(variance + (double)eps);
+    for (int64_t c = 0; c < cols; ++c) {
+      const double normal = ((double)row[c] - mean) * factor;
+      const double value = normal * (weight ? (double)weight[c] : 1.0) + (bias ? (double)bias[c] : 0.0);
+      out[r * cols + c] = (float)value;
+    }
+  }
+}
+
+/* CpuElementwise.modulate (ops/CpuElementwise.scala:212-217) */
+void oracle_modulate(const float* x, const float* scale, const float* shift, float* out, int64_t rows,
+                     int64_t cols) {
+  for (int64_t r = 0; r < rows; ++r)
+    for (int64_t c = 0; c < cols; ++c) {
+      const int64_t i = r * cols + c;
+      out[i] = (float)((double)x[i] * (1 + (double)scale[c]) + (double)shift[c]);
+    }
+}
+
+/* The section a pair takes its position from (ops/CpuAttention.scala:98-108,
+ * ops/Rope.scala:245-268). */
+static int rope_section(int pair, int sections, const int32_t* s) {
+  switch (sections) {
+    case 1:
+      return pair < s[0] ? 0 : (pair < s[0] + s[1] ? 1 : 2);
+    case 2:
+      if (pair % 3 == 1 && pair < 3 * s[1]) return 1;
+      if (pair % 3 == 2 && pair < 3 * s[2]) return 2;
+      return 0;
+    case 3: {
+      int end = 0;
+      for (int a = 0; a < 4; ++a) {
+        end += s[a];
+        if (pair < end) return a;
+      }
+      return -1;
+    }
+    default:
+      return 0;
+  }
+}
+
+/* ops/CpuAttention.scala:124-133: pow in double, rounded to float, then a
+ * float reciprocal. */
+float oracle_rope_inverse_frequency(int pair, int rotary, float theta, int sections, const int32_t* s) {
+  if (sections == 3) {
+    const int axis = rope_section(pair, sections, s);
+    int start = 0;
+    for (int a = 0; a < axis; ++a) start += s[a];
+    const int count = s[axis];
+    return 1.0f / (float)pow((double)theta, (double)(pair - start) / (double)count);
+  }
+  return 1.0f / (float)pow((double)theta, 2.0 * pair / (double)rotary);
+}
+
+/* CpuAttention.rope (ops/CpuAttention.scala:92-146): value d of each head turns
+ * with its partner (NeoX: d +- rotary/2; interleaved: d ^ 1) by the float angle
+ * position * inverse frequency, in double; values from `rotary` on are copied. */
+void oracle_rope(const float* x, const int32_t* positions, float* out, int tokens, int heads, int dim, int rotary,
+                 float theta, int layout, int sections, const int32_t* s) {
+  const int half = rotary / 2;
+  for (int t = 0; t < tokens; ++t)
+    for (int h = 0; h < heads; ++h) {
+      const int64_t base = ((int64_t)t * heads + h) * dim;
+      for (int d = 0; d < dim; ++d) {
+        double value;
+        if (d >= rotary) {
+          value = (double)x[base + d];
+        } else {
+          int pair, first, partner;
+          if (layout == 0) {
+            pair = d % half;
+            first = d < half;
+            partner = first ? d + half : d - half;
+          } else {
+            pair = d / 2;
+            first = d % 2 == 0;
+            partner = first ? d + 1 : d - 1;
+          }
+          const float inverse = oracle_rope_inverse_frequency(pair, rotary, theta, sections, s);
+          const int32_t p = positions[(int64_t)rope_section(pair, sections, s) * tokens + t];
+          const float angle_f = (float)p * inverse;
+          const double angle = (double)angle_f;
+          const double a = first ? (double)x[base + d] : (double)x[base + partner];
+          const double b = first ? (double)x[base + partner] : (double)x[base + d];
+          value = first ? a * cos(angle) - b * sin(angle) : a * sin(angle) + b * cos(angle);
+        }
+        out[base + d] = (float)value;
+      }
+    }
+}
+
+/* CpuAttention.ropeTable (ops/CpuAttention.scala:53-87) */
+void oracle_rope_table(const float* x, const float* cosines, const float* sines, float* out, int tokens, int heads,
+                       int dim, int pairs, int per_head, int halves) {
+  const int64_t count = (int64_t)tokens * heads * dim;
+  for (int64_t index = 0; index < count; ++index) {
+    const int d = (int)(index % dim);
+    const int64_t row = per_head ? index / dim : index / ((int64_t)heads * dim);
+    double value;
+    if (halves) {
+      if (d >= 2 * pairs) {
+        value = (double)x[index];
+      } else {
+        const int m = d % pairs;
+        const double c = (double)cosines[row * pairs + m], s = (double)sines[row * pairs + m];
+        const double a = (double)x[index - d + m], b = (double)x[index - d + m + pairs];
+        value = d < pairs ? a * c - b * s : b * c + a * s;
+      }
+    } else {
+      const int m = d / 2;
+      if (m >= pairs) {
+        value = (double)x[index];
+      } else {
+        const double c = (double)cosines[row * pairs + m], s = (double)sines[row * pairs + m];
+        const double a = (double)x[index - d % 2], b = (double)x[index - d % 2 + 1];
+        value = d % 2 == 0 ? a * c - b * s : a * s + b * c;
+      }
+    }
+    out[index] = (float)value;
+  }
+}
+
+/* WanConfig.ropePairs (models/Wan.scala:35-41): frame, row and column pairs
+ * of a head, d - 4*floor(d/6), 2*floor(d/6), 2*floor(d/6) values, halved. */
+void oracle_wan_pairs(int head_dim, int32_t* pairs3) {
+  const int side = 2 * (head_dim / 6);
+  pairs3[0] = (head_dim - 2 * side) / 2;
+  pairs3[1] = side / 2;
+  pairs3[2] = side / 2;
+}
+
+/* Wan.angles (models/Wan.scala:324-361): per token and pair, the axis
+ * position over theta^(2 index / (2 pairs_axis)) in double, then cos and sin
+ * rounded to float. */
+void oracle_wan_angles(int frames, int rows, int cols, int head_dim, double theta, float* cosines, float* sines) {
+  int32_t axes[3];
+  oracle_wan_pairs(head_dim, axes);
+  const int pairs = head_dim / 2;
+  const int64_t tokens = (int64_t)frames * rows * cols;
+  for (int64_t i = 0; i < tokens * pairs; ++i) {
+    const int64_t token = i / pairs;
+    const int pair = (int)(i % pairs);
+    int axis, index;
+    if (pair < axes[0]) {
+      axis = 0;
+      index = pair;
+    } else if (pair < axes[0] + axes[1]) {
+      axis = 1;
+      index = pair - axes[0];
+    } else {
+      axis = 2;
+      index = pair - axes[0] - axes[1];
+    }
+    int64_t position;
+    if (axis == 0)
+      position = token / ((int64_t)rows * cols);
+    else if (axis == 1)
+      position = token / cols % rows;
+    else
+      position = token % cols;
+    const double angle = (double)position / pow(theta, 2.0 * index / (double)(2 * axes[axis]));
+    cosines[i] = (float)cos(angle);
+    sines[i] = (float)sin(angle);
+  }
+}
+
+/* CpuLinear.embedding (ops/CpuLinear.scala:12-41) over GgmlQuants.Q8_0
+ * (tensor/GgmlQuants.scala:104-118): per 34-byte block, d = f16 at byte 0,
+ * value j = float(int8 at byte 2 + j) * d in float. */
+int64_t oracle_embedding_q8_0(const uint8_t* table, int64_t vocab, int64_t cols, const int32_t* ids, int64_t count,
+                              float* out) {
+  const int64_t blocks = cols / 32;
+  const int64_t row_bytes = blocks * 34;
+  for (int64_t t = 0; t < count; ++t) {
+    const int64_t row = ids[t];
+    if (row < 0 || row >= vocab) return t;
+    const uint8_t* source = table + row * row_bytes;
+    for (int64_t b = 0; b < blocks; ++b) {
+      const uint8_t* block = source + b * 34;
+      const float d = oracle_f16_to_f32((uint16_t)(block[0] | (block[1] << 8)));
+      for (int j = 0; j < 32; ++j) out[t * cols + b * 32 + j] = (float)(int8_t)block[2 + j] * d;
+    }
+  }
+  return -1;
+}
+
+int64_t oracle_embedding_f32(const float* table, int64_t vocab, int64_t cols, const int32_t* ids, int64_t count,
+                             float* out) {
+  for (int64_t t = 0; t < count; ++t) {
+    const int64_t row = ids[t];
+    if (row < 0 || row >= vocab) return t;
+    memcpy(out + t * cols, table + row * cols, (size_t)cols * 4);
+  }
+  return -1;
+}

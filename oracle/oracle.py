@@ -1,0 +1,381 @@
+"""Test infrastructure only: numpy front end of the CPU oracle (cpu_ops.c).
+
+The oracle restates the drift runner's CPU reference backend (`CpuOps`,
+ops/CpuOps.scala) for the fused layer kernels' path. Tests compare the HIP
+kernels with it, bench.py times it as the CPU baseline, and
+__graft_entry__.smoke() checks one launch against it. The product never
+imports this module.
+
+Compositions for the bf16 configurations follow the reference's own bf16
+path: `convert` BF16 -> F32 (tensor/DType.scala:99-102), the F32 op, then
+`convert` F32 -> BF16 (ops/CpuMemory.scala:84-109, CpuOps.toBfloat16).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "libdrift_oracle.so")
+
+SILU, GELU_TANH, GELU_ERF, SIGMOID, SITU = range(5)
+NEOX, INTERLEAVED = 0, 1
+SINGLE, CONTIGUOUS, INTERLEAVED_MROPE, AXES = range(4)
+
+
+def build() -> str:
+    """Compile cpu_ops.c with the Makefile beside it; return the library path."""
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+    return _LIB_PATH
+
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        _lib = ctypes.CDLL(_LIB_PATH)
+        _declare(_lib)
+    return _lib
+
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_I32 = ctypes.c_int
+_F32 = ctypes.c_float
+_F64 = ctypes.c_double
+
+
+def _declare(l: ctypes.CDLL) -> None:
+    sig = {
+        "oracle_to_bf16": (ctypes.c_uint16, [_F32]),
+        "oracle_from_bf16": (_F32, [ctypes.c_uint16]),
+        "oracle_f16_to_f32": (_F32, [ctypes.c_uint16]),
+        "oracle_f32_to_f16": (ctypes.c_uint16, [_F32]),
+        "oracle_f32_to_bf16_n": (None, [_P, _P, _I64]),
+        "oracle_bf16_to_f32_n": (None, [_P, _P, _I64]),
+        "oracle_f32_to_f16_n": (None, [_P, _P, _I64]),
+        "oracle_f16_to_f32_n": (None, [_P, _P, _I64]),
+        "oracle_erf": (_F64, [_F64]),
+        "oracle_activate": (_F64, [_I32, _F64]),
+        "oracle_activation": (None, [_I32, _F32, _P, _P, _I64]),
+        "oracle_gated": (None, [_I32, _P, _P, _P, _I64]),
+        "oracle_rms_norm": (None, [_P, _P, _P, _P, _I64, _I64, _F32, _F32, _I64]),
+        "oracle_layer_norm": (None, [_P, _P, _P, _P, _I64, _I64, _F32]),
+        "oracle_modulate": (None, [_P, _P, _P, _P, _I64, _I64]),
+        "oracle_rope": (None, [_P, _P, _P, _I32, _I32, _I32, _I32, _F32, _I32, _I32, _P]),
+        "oracle_rope_inverse_frequency": (_F32, [_I32, _I32, _F32, _I32, _P]),
+        "oracle_rope_table": (None, [_P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _I32]),
+        "oracle_wan_pairs": (None, [_I32, _P]),
+        "oracle_wan_angles": (None, [_I32, _I32, _I32, _I32, _F64, _P, _P]),
+        "oracle_embedding_q8_0": (_I64, [_P, _I64, _I64, _P, _I64, _P]),
+        "oracle_embedding_f32": (_I64, [_P, _I64, _I64, _P, _I64, _P]),
+    }
+    for name, (restype, argtypes) in sig.items():
+        fn = getattr(l, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+
+
+def _ptr(a: np.ndarray | None):
+    return None if a is None else a.ctypes.data
+
+
+def _c(a, dtype) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=dtype)
+
+
+# ---------------------------------------------------------------- conversions
+
+def to_bf16(x) -> np.ndarray:
+    """F32 -> BF16 bits, CpuOps.toBfloat16 (ops/CpuOps.scala:426-431)."""
+    x = _c(x, np.float32)
+    out = np.empty(x.shape, np.uint16)
+    lib().oracle_f32_to_bf16_n(_ptr(x), _ptr(out), x.size)
+    return out
+
+
+def from_bf16(bits) -> np.ndarray:
+    """BF16 bits -> F32 (tensor/DType.scala:99-102)."""
+    bits = _c(bits, np.uint16)
+    out = np.empty(bits.shape, np.float32)
+    lib().oracle_bf16_to_f32_n(_ptr(bits), _ptr(out), bits.size)
+    return out
+
+
+def to_f16(x) -> np.ndarray:
+    x = _c(x, np.float32)
+    out = np.empty(x.shape, np.uint16)
+    lib().oracle_f32_to_f16_n(_ptr(x), _ptr(out), x.size)
+    return out
+
+
+def from_f16(bits) -> np.ndarray:
+    """F16 bits -> F32, Float.float16ToFloat (tensor/LittleEndian.scala:147-148)."""
+    bits = _c(bits, np.uint16)
+    out = np.empty(bits.shape, np.float32)
+    lib().oracle_f16_to_f32_n(_ptr(bits), _ptr(out), bits.size)
+    return out
+
+
+def erf(x: float) -> float:
+    return lib().oracle_erf(x)
+
+
+def activate(kind: int, v: float) -> float:
+    return lib().oracle_activate(kind, v)
+
+
+# ---------------------------------------------------------------- F32 ops
+
+def activation(kind: int, x, input_scale: float = 1.0) -> np.ndarray:
+    x = _c(x, np.float32)
+    out = np.empty_like(x)
+    lib().oracle_activation(kind, input_scale, _ptr(x), _ptr(out), x.size)
+    return out
+
+
+def gated(kind: int, gate, up) -> np.ndarray:
+    gate, up = _c(gate, np.float32), _c(up, np.float32)
+    assert gate.shape == up.shape
+    out = np.empty_like(gate)
+    lib().oracle_gated(kind, _ptr(gate), _ptr(up), _ptr(out), gate.size)
+    return out
+
+
+def rms_norm(x, weight, eps: float, offset: float = 0.0, y=None, weight_rows: int = 1):
+    """Returns `out`, or `(x + y, out)` when `y` is given (addRmsNorm)."""
+    x = np.array(x, dtype=np.float32, copy=True, order="C")
+    weight = _c(weight, np.float32)
+    cols = x.shape[-1]
+    rows = x.size // cols if cols else 0
+    yy = None if y is None else _c(y, np.float32)
+    out = np.empty_like(x)
+    lib().oracle_rms_norm(_ptr(x), _ptr(yy), _ptr(weight), _ptr(out), rows, cols, eps, offset, weight_rows)
+    return out if y is None else (x, out)
+
+
+def layer_norm(x, weight=None, bias=None, eps: float = 1e-5) -> np.ndarray:
+    x = _c(x, np.float32)
+    w = None if weight is None else _c(weight, np.float32)
+    b = None if bias is None else _c(bias, np.float32)
+    cols = x.shape[-1]
+    out = np.empty_like(x)
+    lib().oracle_layer_norm(_ptr(x), _ptr(w), _ptr(b), _ptr(out), x.size // cols, cols, eps)
+    return out
+
+
+def modulate(x, scale, shift) -> np.ndarray:
+    x = _c(x, np.float32)
+    scale, shift = _c(scale, np.float32), _c(shift, np.float32)
+    cols = x.shape[-1]
+    out = np.empty_like(x)
+    lib().oracle_modulate(_ptr(x), _ptr(scale), _ptr(shift), _ptr(out), x.size // cols, cols)
+    return out
+
+
+def _sections(sizes) -> np.ndarray:
+    s = np.zeros(4, np.int32)
+    s[: len(sizes)] = sizes
+    return s
+
+
+def rope(x, positions, theta: float, rotary: int, layout: int = NEOX, sections: int = SINGLE, sizes=()):
+    x = _c(x, np.float32)
+    positions = _c(positions, np.int32)
+    tokens, heads, dim = x.shape
+    out = np.empty_like(x)
+    lib().oracle_rope(_ptr(x), _ptr(positions), _ptr(out), tokens, heads, dim, rotary, theta, layout,
+                      sections, _ptr(_sections(sizes)))
+    return out
+
+
+def rope_inverse_frequency(pair: int, rotary: int, theta: float, sections: int = SINGLE, sizes=()) -> float:
+    return lib().oracle_rope_inverse_frequency(pair, rotary, theta, sections, _ptr(_sections(sizes)))
+
+
+def rope_table(x, cosines, sines, halves: bool = False) -> np.ndarray:
+    x = _c(x, np.float32)
+    cosines, sines = _c(cosines, np.float32), _c(sines, np.float32)
+    tokens, heads, dim = x.shape
+    pairs = cosines.shape[-1]
+    per_head = 1 if cosines.ndim == 3 else 0
+    out = np.empty_like(x)
+    lib().oracle_rope_table(_ptr(x), _ptr(cosines), _ptr(sines), _ptr(out), tokens, heads, dim, pairs, per_head,
+                            1 if halves else 0)
+    return out
+
+
+def wan_pairs(head_dim: int = 128):
+    p = np.zeros(3, np.int32)
+    lib().oracle_wan_pairs(head_dim, _ptr(p))
+    return tuple(int(v) for v in p)
+
+
+def wan_angles(frames: int, rows: int, cols: int, head_dim: int = 128, theta: float = 10000.0):
+    tokens = frames * rows * cols
+    cos = np.empty((tokens, head_dim // 2), np.float32)
+    sin = np.empty((tokens, head_dim // 2), np.float32)
+    lib().oracle_wan_angles(frames, rows, cols, head_dim, theta, _ptr(cos), _ptr(sin))
+    return cos, sin
+
+
+def embedding_q8_0(table, vocab: int, cols: int, ids) -> np.ndarray:
+    table = _c(table, np.uint8)
+    ids = _c(ids, np.int32)
+    assert table.size == vocab * cols // 32 * 34
+    out = np.empty((ids.size, cols), np.float32)
+    bad = lib().oracle_embedding_q8_0(_ptr(table), vocab, cols, _ptr(ids), ids.size, _ptr(out))
+    if bad >= 0:
+        raise ValueError(f"token id {int(ids[bad])} outside the table")
+    return out
+
+
+def embedding_f32(table, ids) -> np.ndarray:
+    table = _c(table, np.float32)
+    ids = _c(ids, np.int32)
+    vocab, cols = table.shape
+    out = np.empty((ids.size, cols), np.float32)
+    bad = lib().oracle_embedding_f32(_ptr(table), vocab, cols, _ptr(ids), ids.size, _ptr(out))
+    if bad >= 0:
+        raise ValueError(f"token id {int(ids[bad])} outside the table")
+    return out
+
+
+# ---------------------------------------------------------------- bf16 compositions
+# The reference has no bf16 kernels: its bf16 path is convert -> F32 op ->
+# convert (ops/HipBase.scala:268-274, kernels/elementwise.hip:68-86).
+
+def rms_norm_bf16(x_bits, weight, eps, offset=0.0, y_bits=None, weight_rows=1):
+    x = from_bf16(x_bits)
+    if y_bits is None:
+        return to_bf16(rms_norm(x, weight, eps, offset, weight_rows=weight_rows))
+    summed, out = rms_norm(x, weight, eps, offset, y=from_bf16(y_bits), weight_rows=weight_rows)
+    return to_bf16(summed), to_bf16(out)
+
+
+def activation_bf16(kind, x_bits, input_scale=1.0):
+    return to_bf16(activation(kind, from_bf16(x_bits), input_scale))
+
+
+def gated_bf16(kind, gate_bits, up_bits):
+    return to_bf16(gated(kind, from_bf16(gate_bits), from_bf16(up_bits)))
+
+
+def layer_norm_modulate(x, scale, shift, rows_per_sample: int, eps: float):
+    """AdaLN as Wan runs it (models/Wan.scala:431-432): layerNorm without
+    affine, F32 written, then modulate with each sample's scale and shift rows
+    (`scale`, `shift` [samples, cols]) over that sample's rows."""
+    x = _c(x, np.float32)
+    scale, shift = np.atleast_2d(_c(scale, np.float32)), np.atleast_2d(_c(shift, np.float32))
+    normed = layer_norm(x, None, None, eps)
+    out = np.empty_like(normed)
+    rows = normed.shape[0]
+    for s in range(math.ceil(rows / rows_per_sample)):
+        lo, hi = s * rows_per_sample, min(rows, (s + 1) * rows_per_sample)
+        out[lo:hi] = modulate(normed[lo:hi], scale[s], shift[s])
+    return out
+
+
+def layer_norm_modulate_bf16(x_bits, scale, shift, rows_per_sample, eps):
+    return to_bf16(layer_norm_modulate(from_bf16(x_bits), scale, shift, rows_per_sample, eps))
+
+
+def qk_norm_rope(q, k, q_weight, k_weight, positions, eps, offset, theta, rotary, layout=NEOX,
+                 sections=SINGLE, sizes=()):
+    """The reference's composition for attention inputs
+    (ops/AttentionOps.scala:87-107): per-head rmsNorm in place (F32 written),
+    then rope of queries and keys. q [t, heads, D], k [t, kvHeads, D]."""
+    q = _c(q, np.float32)
+    k = _c(k, np.float32)
+    t, heads, d = q.shape
+    kv = k.shape[1]
+    qn = rms_norm(q.reshape(t * heads, d), q_weight, eps, offset).reshape(t, heads, d)
+    kn = rms_norm(k.reshape(t * kv, d), k_weight, eps, offset).reshape(t, kv, d)
+    return (rope(qn, positions, theta, rotary, layout, sections, sizes),
+            rope(kn, positions, theta, rotary, layout, sections, sizes))
+
+
+def qk_norm_rope_bf16(q_bits, k_bits, q_weight, k_weight, positions, eps, offset, theta, rotary, layout=NEOX,
+                      sections=SINGLE, sizes=()):
+    rq, rk = qk_norm_rope(from_bf16(q_bits), from_bf16(k_bits), q_weight, k_weight, positions, eps, offset, theta,
+                          rotary, layout, sections, sizes)
+    return to_bf16(rq), to_bf16(rk)
+
+
+def rope_3d(x, frames, rows, cols, theta=10000.0, token_offset=0):
+    """Wan's 3-D RoPE (models/Wan.scala:324-361, :442-443): the angle tables
+    of the frames x rows x cols grid, then ropeTable with adjacent pairs.
+    x [tokens, heads, D]; token i sits at grid index token_offset + i."""
+    x = _c(x, np.float32)
+    tokens, heads, d = x.shape
+    cos, sin = wan_angles(frames, rows, cols, d, theta)
+    grid = frames * rows * cols
+    index = (token_offset + np.arange(tokens)) % grid
+    return rope_table(x, cos[index], sin[index], halves=False)
+
+
+def rope_3d_bf16(x_bits, frames, rows, cols, theta=10000.0, token_offset=0):
+    return to_bf16(rope_3d(from_bf16(x_bits), frames, rows, cols, theta, token_offset))
+
+
+def embedding_q8_0_bf16(table, vocab, cols, ids):
+    """The F32 gather converted to BF16: bit-exact by construction, since the
+    product of an fp16 scale and an int8 code is exact in F32."""
+    return to_bf16(embedding_q8_0(table, vocab, cols, ids))
+
+
+# ---------------------------------------------------------------- inputs
+
+def java_gaussian(seed: int, count: int) -> np.ndarray:
+    """TestData.gaussian (runner/test/src/drift/runner/TestData.scala:10-13):
+    `scala.util.Random(seed).nextGaussian().toFloat`, i.e. java.util.Random's
+    48-bit LCG and its polar Box-Muller. StrictMath.log is replaced by the C
+    library's log; both are within an ulp in double, far below a float's."""
+    mask = (1 << 48) - 1
+    state = (seed ^ 0x5DEECE66D) & mask
+
+    def nxt(bits):
+        nonlocal state
+        state = (state * 0x5DEECE66D + 0xB) & mask
+        return state >> (48 - bits)
+
+    def next_double():
+        return ((nxt(26) << 27) + nxt(27)) * (1.0 / (1 << 53))
+
+    out = np.empty(count, np.float32)
+    spare = None
+    for i in range(count):
+        if spare is not None:
+            out[i] = np.float32(spare)
+            spare = None
+            continue
+        while True:
+            v1 = 2 * next_double() - 1
+            v2 = 2 * next_double() - 1
+            s = v1 * v1 + v2 * v2
+            if 0 < s < 1:
+                break
+        multiplier = math.sqrt(-2 * math.log(s) / s)
+        spare = v2 * multiplier
+        out[i] = np.float32(v1 * multiplier)
+    return out
+
+
+def q8_0_table(rows: int, cols: int, rng: np.random.Generator, scale_lo=1e-3, scale_hi=2e-2) -> np.ndarray:
+    """A Q8_0 table: codes uniform in [-127, 127], fp16 scales uniform in
+    [scale_lo, scale_hi], as bytes [rows, cols/32*34]."""
+    blocks = rows * (cols // 32)
+    raw = np.empty((blocks, 34), np.uint8)
+    scales = rng.uniform(scale_lo, scale_hi, blocks).astype(np.float16)
+    raw[:, 0:2] = scales.view(np.uint8).reshape(blocks, 2)
+    raw[:, 2:] = rng.integers(-127, 128, (blocks, 32)).astype(np.int8).view(np.uint8)
+    return raw.reshape(rows, cols // 32 * 34)
