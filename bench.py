@@ -1,0 +1,326 @@
+"""Benchmark of the drift runner's fused layer kernels on one MI355X.
+
+A step is one pass of the path over its configurations, every kernel once:
+  C2  decode bf16: RMSNorm [B, 4096] and SwiGLU [B, 14336], B = 1, 8, 64
+  C3  prefill bf16: per-head RMSNorm + NeoX RoPE, Q [4096, 32, 128], K [4096, 8, 128]
+  C4  Q8_0 gather of 8192 ids from [151936, 4096] to bf16
+  C5  Video DiT block bf16: AdaLN [65520, 3072], GELU-tanh in place, 3-D RoPE
+      Q [65520, 24, 128] on the 21 x 30 x 52 grid
+Inputs are synthetic (seeded device generators) and resident in HBM. Each
+kernel rotates through buffer sets totalling more than 512 MB, so the 256 MB
+Infinity Cache cannot hold what the next launch reads.
+
+Printed: one JSON line. `value` is the step's algorithmic bytes (the reads
+and writes of the tensors each op names) over the step's wall time;
+`kernels` has each kernel's HIP-event time, GB/s, fraction of the 8 TB/s HBM
+peak and rows/s; `roofline` is the dominant kernel's; `cpu_baseline` is the
+CPU reference arithmetic (the oracle) timed on a bounded sample of the same
+work on this host's cores, scaled to the whole step.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+from drift_amd import ops as d  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+MALL_BYTES = 512 << 20
+DEV = "cuda:0"
+
+
+class Kernel:
+    """One fused kernel at one configuration: its launch over buffer set i,
+    its algorithmic bytes and rows per launch, and a CPU reference leg."""
+
+    def __init__(self, name, config, bytes_per_call, rows, launch, cpu=None):
+        self.name, self.config = name, config
+        self.bytes, self.rows = bytes_per_call, rows
+        self.launch = launch
+        self.cpu = cpu  # (sample description, seconds for the sample, fraction of a call the sample is)
+        self.times_ms = []
+
+
+def sets_for(bytes_per_call: int, floor: int = 2) -> int:
+    return max(floor, math.ceil(MALL_BYTES / max(bytes_per_call, 1)) + 1)
+
+
+def gen(seed):
+    g = torch.Generator(device=DEV)
+    g.manual_seed(seed)
+    return g
+
+
+def randn_bf16(shape, seed, scale=1.0):
+    return (scale * torch.randn(shape, generator=gen(seed), device=DEV)).to(torch.bfloat16)
+
+
+def make_kernels(hip: d.HipOps):
+    kernels = []
+
+    # C2 decode: RMSNorm bf16 [B, 4096] (w f32, eps 1e-5) and SwiGLU [B, 14336]
+    for b in (1, 8, 64):
+        nbytes = 2 * b * 4096 * 2 + 4096 * 4
+        n = sets_for(nbytes, 8)
+        xs = [randn_bf16((b, 4096), 10 + i) for i in range(n)]
+        outs = [torch.empty_like(xs[0]) for _ in range(n)]
+        w = (1 + 0.1 * torch.randn(4096, generator=gen(1), device=DEV)).float()
+        kernels.append(Kernel(f"rms_norm_bf16_b{b}", f"C2 RMSNorm bf16 [{b},4096] eps 1e-5", nbytes, b,
+                              lambda i, xs=xs, outs=outs, w=w: hip.rmsNorm(xs[i % len(xs)], w, 1e-5, 0.0,
+                                                                           outs[i % len(outs)])))
+        nbytes = 3 * b * 14336 * 2
+        n = sets_for(nbytes, 8)
+        gs = [randn_bf16((b, 14336), 100 + i) for i in range(n)]
+        us = [randn_bf16((b, 14336), 200 + i) for i in range(n)]
+        os_ = [torch.empty_like(gs[0]) for _ in range(n)]
+        kernels.append(Kernel(f"swiglu_bf16_b{b}", f"C2 SwiGLU bf16 [{b},14336]", nbytes, b,
+                              lambda i, gs=gs, us=us, os_=os_: hip.gated(d.Activation.Silu, gs[i % len(gs)],
+                                                                         us[i % len(us)], os_[i % len(os_)])))
+
+    # C3 prefill: per-head RMSNorm (eps 1e-6) + NeoX RoPE (theta 1e6)
+    t, hq, hk, dim = 4096, 32, 8, 128
+    nbytes = 2 * (t * (hq + hk) * dim * 2) + t * 4 + 2 * dim * 4
+    n = sets_for(nbytes)
+    qs = [randn_bf16((t, hq, dim), 300 + i) for i in range(n)]
+    ks = [randn_bf16((t, hk, dim), 400 + i) for i in range(n)]
+    rqs = [torch.empty_like(qs[0]) for _ in range(n)]
+    rks = [torch.empty_like(ks[0]) for _ in range(n)]
+    qw = (1 + 0.1 * torch.randn(dim, generator=gen(2), device=DEV)).float()
+    kw = (1 + 0.1 * torch.randn(dim, generator=gen(3), device=DEV)).float()
+    positions = torch.arange(t, dtype=torch.int32, device=DEV)
+    norms = d.QueryKeyNorms(qw, kw, 1e-6, 0.0, d.Rope(1e6, 128, d.RopeLayout.Neox))
+    kernels.append(Kernel("qk_norm_rope_bf16", "C3 per-head RMSNorm + NeoX RoPE bf16 Q[4096,32,128] K[4096,8,128]",
+                          nbytes, t,
+                          lambda i, n=n: hip.queryKeyNormRope(qs[i % n], ks[i % n], norms, positions, rqs[i % n],
+                                                              rks[i % n])))
+
+    # C4: Q8_0 gather, 8192 ids from [151936, 4096] to bf16
+    vocab, cols, count = 151936, 4096, 8192
+    blocks = cols // 32
+    table = torch.empty((vocab, blocks, 34), dtype=torch.uint8, device=DEV)
+    g = gen(4)
+    for lo in range(0, vocab, 16384):
+        hi = min(vocab, lo + 16384)
+        table[lo:hi, :, 2:] = torch.randint(-127, 128, (hi - lo, blocks, 32), generator=g, device=DEV,
+                                            dtype=torch.int32).to(torch.int8).view(torch.uint8)
+        sc = (1e-3 + (2e-2 - 1e-3) * torch.rand((hi - lo, blocks), generator=g, device=DEV)).half()
+        table[lo:hi, :, 0:2] = sc.view(torch.uint8).view(hi - lo, blocks, 2)
+    q8 = d.Q8_0Table(table.view(vocab, blocks * 34), cols)
+    nbytes = count * blocks * 34 + count * 4 + count * cols * 2
+    n = sets_for(nbytes)
+    idss = [torch.randint(0, vocab, (count,), generator=gen(500 + i), device=DEV, dtype=torch.int32)
+            for i in range(n)]
+    gouts = [torch.empty((count, cols), dtype=torch.bfloat16, device=DEV) for _ in range(n)]
+    kernels.append(Kernel("embedding_q8_0_bf16", "C4 Q8_0 gather 8192 ids from [151936,4096] to bf16", nbytes,
+                          count, lambda i, n=n: hip.embedding(q8, idss[i % n], gouts[i % n])))
+
+    # C5: Video DiT block, x [2 * 32760, 3072]
+    rows, width, per = 2 * 32760, 3072, 32760
+    n = 2
+    xs5 = [randn_bf16((rows, width), 600 + i) for i in range(n)]
+    outs5 = [torch.empty_like(xs5[0]) for _ in range(n)]
+    shift = (0.1 * torch.randn((2, width), generator=gen(5), device=DEV)).float()
+    scale = (0.1 * torch.randn((2, width), generator=gen(6), device=DEV)).float()
+    nbytes = 2 * rows * width * 2 + 2 * 2 * width * 4
+    kernels.append(Kernel("adaln_bf16", "C5 AdaLN LN(eps 1e-6)*(1+scale)+shift bf16 [65520,3072]", nbytes, rows,
+                          lambda i, n=n: hip.layerNormModulate(xs5[i % n], scale, shift, 1e-6, outs5[i % n], per)))
+    nbytes = 2 * rows * width * 2
+    kernels.append(Kernel("gelu_tanh_bf16", "C5 GELU-tanh bf16 in place [65520,3072]", nbytes, rows,
+                          lambda i, n=n: hip.activation(d.Activation.GeluTanh, outs5[i % n], outs5[i % n])))
+    qs5 = [randn_bf16((rows, 24, 128), 700 + i) for i in range(n)]
+    rq5 = [torch.empty_like(qs5[0]) for _ in range(n)]
+    nbytes = 2 * rows * 24 * 128 * 2
+    kernels.append(Kernel("rope_3d_bf16", "C5 3-D RoPE bf16 Q[65520,24,128] grid 21x30x52 theta 1e4", nbytes, rows,
+                          lambda i, n=n: hip.rope3d(qs5[i % n], 21, 30, 52, rq5[i % n])))
+    return kernels
+
+
+# ------------------------------------------------------------------ CPU baseline
+
+def cpu_baseline(kernels, budget_s: float):
+    """The oracle (the reference's CPU arithmetic, restated in C) on a bounded
+    sample of each kernel's work, on one core, scaled to the whole launch:
+    rows are independent in every op, so time grows with rows. Each sample
+    is sized to take about budget_s / 13 seconds."""
+    from oracle import oracle as o
+
+    rng = np.random.default_rng(0)
+
+    def bits(shape):
+        return o.to_bf16(rng.standard_normal(shape).astype(np.float32))
+
+    w4096 = (1 + 0.1 * rng.standard_normal(4096)).astype(np.float32)
+    w128 = (1 + 0.1 * rng.standard_normal(128)).astype(np.float32)
+    sc = (0.1 * rng.standard_normal((1, 3072))).astype(np.float32)
+    table = o.q8_0_table(4096, 4096, rng)
+
+    def rms(units):
+        x = bits((units, 4096))
+        return lambda: o.rms_norm_bf16(x, w4096, 1e-5)
+
+    def swiglu(units):
+        g, u = bits((units, 14336)), bits((units, 14336))
+        return lambda: o.gated_bf16(0, g, u)
+
+    def qk(units):
+        q, k = bits((units, 32, 128)), bits((units, 8, 128))
+        p = np.arange(units, dtype=np.int32)
+        return lambda: o.qk_norm_rope_bf16(q, k, w128, w128, p, 1e-6, 0.0, 1e6, 128)
+
+    def gather(units):
+        ids = rng.integers(0, 4096, units).astype(np.int32)
+        return lambda: o.embedding_q8_0_bf16(table, 4096, 4096, ids)
+
+    def adaln(units):
+        x = bits((units, 3072))
+        return lambda: o.layer_norm_modulate_bf16(x, sc, sc, units, 1e-6)
+
+    def gelu(units):
+        x = bits((units, 3072))
+        return lambda: o.activation_bf16(1, x)
+
+    def rope3d(units):
+        x = bits((units, 24, 128))
+        return lambda: o.rope_3d_bf16(x, 21, 30, 52)
+
+    work = {}
+    for b in (1, 8, 64):
+        work[f"rms_norm_bf16_b{b}"] = (rms, b, "rows")
+        work[f"swiglu_bf16_b{b}"] = (swiglu, b, "rows")
+    work.update({"qk_norm_rope_bf16": (qk, 4096, "tokens"), "embedding_q8_0_bf16": (gather, 8192, "ids"),
+                 "adaln_bf16": (adaln, 65520, "rows"), "gelu_tanh_bf16": (gelu, 65520, "rows"),
+                 "rope_3d_bf16": (rope3d, 65520, "tokens")})
+    target = budget_s / 13
+    for k in kernels:
+        make, total, unit = work[k.name]
+        probe = min(total, 8)
+        fn = make(probe)
+        t0 = time.perf_counter()
+        fn()
+        per_unit = (time.perf_counter() - t0) / probe
+        units = int(min(total, max(probe, target / max(per_unit, 1e-9))))
+        fn = make(units)
+        t0 = time.perf_counter()
+        fn()
+        seconds = time.perf_counter() - t0
+        k.cpu = (f"{units} of {total} {unit}", seconds, units / total)
+
+
+# ------------------------------------------------------------------ main
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU reference work, about")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--only", default="", help="comma-separated kernel names to run (profiling)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this path runs on one GPU; --gpus {args.gpus} is not supported "
+              f"(rows shard across GPUs with no exchange, so N GPUs do N times the work)", file=sys.stderr)
+        sys.exit(2)
+
+    torch.cuda.set_device(0)
+    hip = d.HipOps()
+    kernels = make_kernels(hip)
+    if args.only:
+        keep = set(args.only.split(","))
+        kernels = [k for k in kernels if k.name in keep]
+    torch.cuda.synchronize()
+
+    call = 0
+    for _ in range(args.warmup):
+        for k in kernels:
+            k.launch(call)
+        call += 1
+    torch.cuda.synchronize()
+
+    stream = torch.cuda.current_stream()
+    events = []
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        for k in kernels:
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record(stream)
+            k.launch(call)
+            end.record(stream)
+            events.append((k, start, end))
+        call += 1
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    for k, start, end in events:
+        k.times_ms.append(start.elapsed_time(end))
+
+    if not args.no_cpu:
+        cpu_baseline(kernels, args.cpu_budget)
+
+    step_bytes = sum(k.bytes for k in kernels)
+    ms_per_step = wall * 1e3 / args.steps
+    table = {}
+    for k in kernels:
+        avg = float(np.mean(k.times_ms))
+        gbs = k.bytes / (avg * 1e-3) / 1e9
+        table[k.name] = {
+            "config": k.config, "us": round(avg * 1e3, 2), "bytes": k.bytes, "GB_s": round(gbs, 1),
+            "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "rows_per_s": round(k.rows / (avg * 1e-3), 1),
+        }
+    dominant = max(kernels, key=lambda k: np.mean(k.times_ms))
+    dom_avg = float(np.mean(dominant.times_ms))
+    achieved = dominant.bytes / (dom_avg * 1e-3) / 1e9
+    traffic = None
+    traffic_file = os.path.join(ROOT, "profiles", "traffic.json")
+    if os.path.exists(traffic_file):
+        with open(traffic_file) as f:
+            traffic = json.load(f).get(dominant.name)
+    line = {
+        "metric": "achieved HBM GB/s and % of MI355X peak per fused kernel; rows/sec at 1 GPU",
+        "value": round(step_bytes / (ms_per_step * 1e-3) / 1e9, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded device generators), resident in HBM; buffer sets rotated past the 256 MB MALL",
+        "config": {
+            "workload": "drift fused layer kernels, one pass over C2 (decode B=1,8,64), C3 (prefill QK norm+RoPE), "
+                        "C4 (Q8_0 gather), C5 (Video DiT AdaLN, GELU-tanh, 3-D RoPE)",
+            "step_bytes": step_bytes,
+            "parallelism": "single GPU",
+        },
+        "kernels": table,
+        "roofline": {
+            "kernel": dominant.name, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+            "algorithmic_bytes_per_launch": dominant.bytes, "avg_launch_us": round(dom_avg * 1e3, 2),
+        },
+    }
+    if not args.no_cpu and all(k.cpu for k in kernels):
+        cpu_step_s = sum(k.cpu[1] / k.cpu[2] for k in kernels)
+        line["cpu_baseline"] = {
+            "value": round(step_bytes / cpu_step_s / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": "; ".join(f"{k.name}: {k.cpu[0]} in {k.cpu[1]:.3f} s" for k in kernels),
+            "step_seconds": round(cpu_step_s, 2),
+        }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

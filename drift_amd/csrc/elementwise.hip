@@ -1,0 +1,283 @@
+// Elementwise kernels for gfx950: activations, gated activations (SwiGLU and
+// kin) and float-type conversions. Each thread streams 16-byte chunks
+// (8 bf16 or 4 F32 values) with a grid-stride loop, two chunks in flight.
+//
+// The runner's CPU reference computes activations in double
+// (ops/CpuNormalisation.scala:11-24). Here they run in float through forms
+// that keep relative accuracy everywhere (no 1 + tanh or 1 + erf
+// cancellation):
+//   silu(v)      = v s(v),   s(v) = 1/(1 + e^-v) from e = e^-|v|
+//   gelu_tanh(v) = v/2 (1 + tanh u) with 1 + tanh u = 2/(1 + e^-2u) or
+//                  2e^2u/(1 + e^2u)
+//   gelu_erf(v)  = v/2 erfc(-v/sqrt2)
+// and, where the reference's own double result is quantized (1 + tanh u and
+// 1 + erf x below 2^-29 hold a whole number of 2^-53 steps, the spacing of
+// doubles just above -1), the same quantization is applied, so the results
+// agree with the reference there too. BF16 outputs use the hardware exp and
+// reciprocal (about 1e-6 relative, far below a bf16 ulp); F32 outputs use the
+// accurate library functions.
+#include "common.hpp"
+
+namespace drift {
+namespace {
+
+template <bool ACCURATE>
+__device__ __forceinline__ float exp_of(float x) {
+  if constexpr (ACCURATE)
+    return expf(x);
+  else
+    return __expf(x);
+}
+
+template <bool ACCURATE>
+__device__ __forceinline__ float divide(float a, float b) {
+  if constexpr (ACCURATE)
+    return a / b;
+  else
+    return __fdividef(a, b);
+}
+
+// A double's 1 + t for t in (-1, -1/2]: a whole number of 2^-53 steps. t here
+// is that sum computed in float; below 2^-29 it is rounded to the step.
+__device__ __forceinline__ float quantize_2m53(float t) {
+  const float steps = rintf(t * 0x1p53f);
+  return t < 0x1p-29f ? steps * 0x1p-53f : t;
+}
+
+template <bool ACCURATE>
+__device__ __forceinline__ float sigmoid_of(float v) {
+  const float e = exp_of<ACCURATE>(-fabsf(v));
+  const float r = divide<ACCURATE>(1.0f, 1.0f + e);
+  return v >= 0.0f ? r : e * r;
+}
+
+template <bool ACCURATE>
+__device__ __forceinline__ float activate(int kind, float v) {
+  switch (kind) {
+    case DRIFT_SILU: {
+      const float e = exp_of<ACCURATE>(-fabsf(v));
+      return divide<ACCURATE>(v >= 0.0f ? v : v * e, 1.0f + e);
+    }
+    case DRIFT_GELU_TANH: {
+      const float u = 0.7978845608028654f * (v + 0.044715f * v * v * v);
+      const float e = exp_of<ACCURATE>(-2.0f * fabsf(u));
+      const float t = divide<ACCURATE>(u >= 0.0f ? 2.0f : 2.0f * e, 1.0f + e);  // 1 + tanh(u)
+      return 0.5f * v * quantize_2m53(t);
+    }
+    case DRIFT_GELU_ERF: {
+      const float t = erfcf(-v * 0.70710678118654752f);  // 1 + erf(v / sqrt 2)
+      return 0.5f * v * quantize_2m53(t);
+    }
+    case DRIFT_SIGMOID:
+      return sigmoid_of<ACCURATE>(v);
+    default:  // DRIFT_SITU: 4 tanh(v / 4) s(v)
+      return 4.0f * tanhf(0.25f * v) * sigmoid_of<ACCURATE>(v);
+  }
+}
+
+template <bool ACCURATE>
+__device__ __forceinline__ float gated_up(int kind, float u) {
+  return kind == DRIFT_SITU ? 25.0f * tanhf(divide<ACCURATE>(u, 25.0f)) : u;
+}
+
+// ------------------------------------------------------------------ kernels
+
+template <typename T>
+constexpr bool kAccurate = sizeof(T) == 4;
+
+template <typename T, int KIND>
+__global__ void __launch_bounds__(256) activation_kernel(const T* x, T* out, int64_t n, int kind, float scale) {
+  constexpr int N = Chunk<T>::N;
+  constexpr bool A = kAccurate<T>;
+  const int k = KIND >= 0 ? KIND : kind;
+  const int64_t chunks = n / N;
+  const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  int64_t i = tid;
+  for (; i + stride < chunks; i += 2 * stride) {
+    float a[N], b[N];
+    Chunk<T>::load(x + i * N, a);
+    Chunk<T>::load(x + (i + stride) * N, b);
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      a[j] = activate<A>(k, scale * a[j]);
+      b[j] = activate<A>(k, scale * b[j]);
+    }
+    Chunk<T>::store(out + i * N, a);
+    Chunk<T>::store(out + (i + stride) * N, b);
+  }
+  if (i < chunks) {
+    float a[N];
+    Chunk<T>::load(x + i * N, a);
+#pragma unroll
+    for (int j = 0; j < N; ++j) a[j] = activate<A>(k, scale * a[j]);
+    Chunk<T>::store(out + i * N, a);
+  }
+  const int64_t tail = chunks * N + tid;
+  if (tail < n) store_one(out + tail, activate<A>(k, scale * load_one(x + tail)));
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256) activation_scalar(const T* x, T* out, int64_t n, int kind, float scale) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+    store_one(out + i, activate<kAccurate<T>>(kind, scale * load_one(x + i)));
+}
+
+template <typename T, int KIND>
+__global__ void __launch_bounds__(256) gated_kernel(const T* gate, const T* up, T* out, int64_t n, int kind) {
+  constexpr int N = Chunk<T>::N;
+  constexpr bool A = kAccurate<T>;
+  const int k = KIND >= 0 ? KIND : kind;
+  const int64_t chunks = n / N;
+  const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = tid; i < chunks; i += stride) {
+    float g[N], u[N];
+    Chunk<T>::load(gate + i * N, g);
+    Chunk<T>::load(up + i * N, u);
+#pragma unroll
+    for (int j = 0; j < N; ++j) g[j] = activate<A>(k, g[j]) * gated_up<A>(k, u[j]);
+    Chunk<T>::store(out + i * N, g);
+  }
+  const int64_t tail = chunks * N + tid;
+  if (tail < n) store_one(out + tail, activate<A>(k, load_one(gate + tail)) * gated_up<A>(k, load_one(up + tail)));
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256) gated_scalar(const T* gate, const T* up, T* out, int64_t n, int kind) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+    store_one(out + i, activate<kAccurate<T>>(kind, load_one(gate + i)) * gated_up<kAccurate<T>>(kind, load_one(up + i)));
+}
+
+// Conversions. F16 through the hardware converts: round to nearest even,
+// subnormals kept.
+__global__ void __launch_bounds__(256) convert_kernel(const void* x, void* out, int64_t n, int kind) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    switch (kind) {
+      case DRIFT_F32_TO_BF16:
+        static_cast<uint16_t*>(out)[i] = (uint16_t)bf16_bits(static_cast<const float*>(x)[i]);
+        break;
+      case DRIFT_BF16_TO_F32:
+        static_cast<float*>(out)[i] = __uint_as_float((uint32_t) static_cast<const uint16_t*>(x)[i] << 16);
+        break;
+      case DRIFT_F32_TO_F16:
+        static_cast<_Float16*>(out)[i] = (_Float16) static_cast<const float*>(x)[i];
+        break;
+      default:
+        static_cast<float*>(out)[i] = (float)static_cast<const _Float16*>(x)[i];
+        break;
+    }
+  }
+}
+
+// 8 values per thread for the F32 <-> BF16 pairs.
+__global__ void __launch_bounds__(256) convert_bf16_chunks(const void* x, void* out, int64_t chunks, int kind) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < chunks; i += stride) {
+    float v[8];
+    if (kind == DRIFT_F32_TO_BF16) {
+      Chunk<float>::load(static_cast<const float*>(x) + i * 8, *reinterpret_cast<float(*)[4]>(v));
+      Chunk<float>::load(static_cast<const float*>(x) + i * 8 + 4, *reinterpret_cast<float(*)[4]>(v + 4));
+      Chunk<uint16_t>::store(static_cast<uint16_t*>(out) + i * 8, v);
+    } else {
+      Chunk<uint16_t>::load(static_cast<const uint16_t*>(x) + i * 8, v);
+      Chunk<float>::store(static_cast<float*>(out) + i * 8, *reinterpret_cast<float(*)[4]>(v));
+      Chunk<float>::store(static_cast<float*>(out) + i * 8 + 4, *reinterpret_cast<float(*)[4]>(v + 4));
+    }
+  }
+}
+
+template <typename T>
+int activation(const char* entry, const T* x, T* out, int64_t n, int32_t kind, float scale, void* stream) {
+  clear_error();
+  if (n < 0) return refuse("%s: %lld values", entry, (long long)n);
+  if (kind < DRIFT_SILU || kind > DRIFT_SITU) return refuse("%s: no activation %d", entry, kind);
+  if (n == 0) return 0;
+  if (!x || !out) return refuse("%s: null x or out", entry);
+  const hipStream_t s = (hipStream_t)stream;
+  constexpr int N = Chunk<T>::N;
+  if (aligned16(x) && aligned16(out)) {
+    const unsigned grid = grid_for(ceil_div(n, 2 * N), 256, 8192);
+    switch (kind) {
+      case DRIFT_SILU:
+        hipLaunchKernelGGL((activation_kernel<T, DRIFT_SILU>), dim3(grid), dim3(256), 0, s, x, out, n, kind, scale);
+        break;
+      case DRIFT_GELU_TANH:
+        hipLaunchKernelGGL((activation_kernel<T, DRIFT_GELU_TANH>), dim3(grid), dim3(256), 0, s, x, out, n, kind,
+                           scale);
+        break;
+      default:
+        hipLaunchKernelGGL((activation_kernel<T, -1>), dim3(grid), dim3(256), 0, s, x, out, n, kind, scale);
+        break;
+    }
+  } else {
+    hipLaunchKernelGGL(activation_scalar<T>, dim3(grid_for(n, 256, 8192)), dim3(256), 0, s, x, out, n, kind, scale);
+  }
+  return launched(entry);
+}
+
+template <typename T>
+int gated(const char* entry, const T* gate, const T* up, T* out, int64_t n, int32_t kind, void* stream) {
+  clear_error();
+  if (n < 0) return refuse("%s: %lld values", entry, (long long)n);
+  if (kind < DRIFT_SILU || kind > DRIFT_SITU) return refuse("%s: no activation %d", entry, kind);
+  if (n == 0) return 0;
+  if (!gate || !up || !out) return refuse("%s: null gate, up or out", entry);
+  const hipStream_t s = (hipStream_t)stream;
+  constexpr int N = Chunk<T>::N;
+  if (aligned16(gate) && aligned16(up) && aligned16(out)) {
+    const unsigned grid = grid_for(ceil_div(n, N), 256, 8192);
+    if (kind == DRIFT_SILU)
+      hipLaunchKernelGGL((gated_kernel<T, DRIFT_SILU>), dim3(grid), dim3(256), 0, s, gate, up, out, n, kind);
+    else
+      hipLaunchKernelGGL((gated_kernel<T, -1>), dim3(grid), dim3(256), 0, s, gate, up, out, n, kind);
+  } else {
+    hipLaunchKernelGGL(gated_scalar<T>, dim3(grid_for(n, 256, 8192)), dim3(256), 0, s, gate, up, out, n, kind);
+  }
+  return launched(entry);
+}
+
+}  // namespace
+}  // namespace drift
+
+using namespace drift;
+
+extern "C" int drift_activation_f32(const float* x, float* out, int64_t n, int32_t kind, float scale,
+                                    void* stream) {
+  return activation<float>("drift_activation_f32", x, out, n, kind, scale, stream);
+}
+
+extern "C" int drift_activation_bf16(const uint16_t* x, uint16_t* out, int64_t n, int32_t kind, float scale,
+                                     void* stream) {
+  return activation<uint16_t>("drift_activation_bf16", x, out, n, kind, scale, stream);
+}
+
+extern "C" int drift_gated_f32(const float* gate, const float* up, float* out, int64_t n, int32_t kind,
+                               void* stream) {
+  return gated<float>("drift_gated_f32", gate, up, out, n, kind, stream);
+}
+
+extern "C" int drift_gated_bf16(const uint16_t* gate, const uint16_t* up, uint16_t* out, int64_t n, int32_t kind,
+                                void* stream) {
+  return gated<uint16_t>("drift_gated_bf16", gate, up, out, n, kind, stream);
+}
+
+extern "C" int drift_convert(const void* x, void* out, int64_t n, int32_t kind, void* stream) {
+  const char* entry = "drift_convert";
+  clear_error();
+  if (n < 0) return refuse("%s: %lld values", entry, (long long)n);
+  if (kind < DRIFT_F32_TO_BF16 || kind > DRIFT_F16_TO_F32) return refuse("%s: no conversion %d", entry, kind);
+  if (n == 0) return 0;
+  if (!x || !out) return refuse("%s: null x or out", entry);
+  if (x == out) return refuse("%s: x and out are the same buffer of different types", entry);
+  const hipStream_t s = (hipStream_t)stream;
+  const bool bf16 = kind == DRIFT_F32_TO_BF16 || kind == DRIFT_BF16_TO_F32;
+  if (bf16 && n % 8 == 0 && aligned16(x) && aligned16(out))
+    hipLaunchKernelGGL(convert_bf16_chunks, dim3(grid_for(n / 8, 256, 8192)), dim3(256), 0, s, x, out, n / 8, kind);
+  else
+    hipLaunchKernelGGL(convert_kernel, dim3(grid_for(n, 256, 8192)), dim3(256), 0, s, x, out, n, kind);
+  return launched(entry);
+}

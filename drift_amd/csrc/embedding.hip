@@ -1,0 +1,141 @@
+// Quantized token-embedding gather for gfx950: rows of a Q8_0 table decoded
+// to F32 or BF16.
+//
+// Q8_0 (tensor/GgmlQuants.scala:104-118): every 32 values are a 34-byte
+// block, an fp16 scale d then 32 int8 codes; value j = float(code j) * d,
+// which is exact in float (11-bit by 8-bit significands), so the BF16 output
+// is bit-exact against the reference's F32 gather rounded to BF16.
+//
+// One wave per id. A row is walked in segments of 128 blocks (4352 bytes,
+// 4096 values): the wave stages the segment in its slice of LDS with 16-byte
+// loads (34-byte blocks are only 2-byte aligned), then each lane decodes
+// 8 consecutive values per step from LDS and stores them as one 16-byte
+// (BF16) or two 16-byte (F32) writes; a store instruction of the wave covers
+// a contiguous 1 or 2 KiB of the output row.
+#include "common.hpp"
+
+namespace drift {
+namespace {
+
+constexpr int kSegmentBlocks = 128;
+constexpr int kSegmentBytes = kSegmentBlocks * 34;  // 4352, a multiple of 16
+
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// float(code) * d as the reference computes it on x86: exact for finite d; an
+// infinite d times code 0 is the x86 default NaN; a NaN d comes back as the
+// float NaN Float.float16ToFloat makes of it (its significand shifted up),
+// quieted by the multiply. nan_bits is that quiet NaN.
+__device__ __forceinline__ float decode(int code, float d, bool special, uint32_t nan_bits) {
+  const float v = (float)code * d;
+  if (!special) return v;
+  if (d != d) return __uint_as_float(nan_bits);
+  return code == 0 ? __uint_as_float(0xffc00000u) : v;
+}
+
+template <typename T>
+__device__ __forceinline__ void store8(T* p, const float (&v)[8]);
+
+template <>
+__device__ __forceinline__ void store8<uint16_t>(uint16_t* p, const float (&v)[8]) {
+  Chunk<uint16_t>::store(p, v);
+}
+
+template <>
+__device__ __forceinline__ void store8<float>(float* p, const float (&v)[8]) {
+  *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+  *reinterpret_cast<float4*>(p + 4) = make_float4(v[4], v[5], v[6], v[7]);
+}
+
+template <typename T, bool ALIGNED>
+__global__ void __launch_bounds__(256) q8_0_gather(const uint8_t* table, const int32_t* ids, T* out, int64_t count,
+                                                   int64_t vocab, int cols, int32_t* bad_id) {
+  __shared__ uint4 stage[4][kSegmentBytes / 16];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  uint8_t* bytes = reinterpret_cast<uint8_t*>(stage[wave]);
+  const uint16_t* halves = reinterpret_cast<const uint16_t*>(stage[wave]);
+  const int blocks = cols / 32;
+  const int64_t row_bytes = (int64_t)blocks * 34;
+  for (int64_t t = (int64_t)blockIdx.x * 4 + wave; t < count; t += (int64_t)gridDim.x * 4) {
+    const int64_t id = ids[t];
+    T* target = out + t * cols;
+    if (id < 0 || id >= vocab) {
+      const float zeros[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+      for (int c = lane; c < cols / 8; c += kWave) store8<T>(target + c * 8, zeros);
+      if (bad_id && lane == 0) *bad_id = 1;
+      continue;
+    }
+    const uint8_t* row = table + id * row_bytes;
+    for (int first = 0; first < blocks; first += kSegmentBlocks) {
+      const int nb = min(kSegmentBlocks, blocks - first);
+      const int seg_bytes = nb * 34;
+      const uint8_t* source = row + (int64_t)first * 34;
+      wave_sync();  // the previous segment has been read
+      if constexpr (ALIGNED) {
+        const int n16 = seg_bytes / 16;
+        for (int i = lane; i < n16; i += kWave) stage[wave][i] = reinterpret_cast<const uint4*>(source)[i];
+        for (int i = n16 * 8 + lane; i < seg_bytes / 2; i += kWave)
+          reinterpret_cast<uint16_t*>(bytes)[i] = reinterpret_cast<const uint16_t*>(source)[i];
+      } else {
+        for (int i = lane; i < seg_bytes / 2; i += kWave)
+          reinterpret_cast<uint16_t*>(bytes)[i] = reinterpret_cast<const uint16_t*>(source)[i];
+      }
+      wave_sync();
+      // 8 values per step: block b = q / 4, its quarter q % 4
+      for (int q = lane; q < nb * 4; q += kWave) {
+        const int b = q >> 2, part = q & 3;
+        const uint32_t h = halves[b * 17];
+        const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+        const uint32_t nan_bits = ((h & 0x8000u) << 16) | 0x7fc00000u | ((h & 0x3ffu) << 13);
+        const bool special = (h & 0x7c00u) == 0x7c00u;
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t pair = halves[b * 17 + 1 + part * 4 + i];
+          v[2 * i] = decode((int)(int8_t)(pair & 0xffu), d, special, nan_bits);
+          v[2 * i + 1] = decode((int)(int8_t)(pair >> 8), d, special, nan_bits);
+        }
+        store8<T>(target + (int64_t)first * 32 + q * 8, v);
+      }
+    }
+  }
+}
+
+template <typename T>
+int embedding_q8_0(const char* entry, const uint8_t* table, const int32_t* ids, T* out, int64_t count,
+                   int64_t vocab, int32_t cols, int32_t* bad_id, void* stream) {
+  clear_error();
+  if (count < 0 || vocab < 0) return refuse("%s: %lld ids into %lld rows", entry, (long long)count, (long long)vocab);
+  if (cols <= 0 || cols % 32 != 0) return refuse("%s: %d values are not whole Q8_0 blocks of 32", entry, cols);
+  if (count == 0) return 0;
+  if (!table || !ids || !out) return refuse("%s: null table, ids or out", entry);
+  if (!aligned16(out)) return refuse("%s: out is not 16-byte aligned", entry);
+  const int64_t row_bytes = (int64_t)cols / 32 * 34;
+  const bool aligned = aligned16(table) && row_bytes % 16 == 0;
+  const dim3 grid(grid_for(count, 4, 1 << 16));
+  const hipStream_t s = (hipStream_t)stream;
+  if (aligned)
+    hipLaunchKernelGGL((q8_0_gather<T, true>), grid, dim3(256), 0, s, table, ids, out, count, vocab, cols, bad_id);
+  else
+    hipLaunchKernelGGL((q8_0_gather<T, false>), grid, dim3(256), 0, s, table, ids, out, count, vocab, cols, bad_id);
+  return launched(entry);
+}
+
+}  // namespace
+}  // namespace drift
+
+using namespace drift;
+
+extern "C" int drift_embedding_q8_0_f32(const uint8_t* table, const int32_t* ids, float* out, int64_t count,
+                                        int64_t vocab, int32_t cols, int32_t* bad_id, void* stream) {
+  return embedding_q8_0<float>("drift_embedding_q8_0_f32", table, ids, out, count, vocab, cols, bad_id, stream);
+}
+
+extern "C" int drift_embedding_q8_0_bf16(const uint8_t* table, const int32_t* ids, uint16_t* out, int64_t count,
+                                         int64_t vocab, int32_t cols, int32_t* bad_id, void* stream) {
+  return embedding_q8_0<uint16_t>("drift_embedding_q8_0_bf16", table, ids, out, count, vocab, cols, bad_id, stream);
+}

@@ -1,0 +1,429 @@
+// Row-wise norms for gfx950: RMSNorm (with the residual add), LayerNorm,
+// AdaLN (LayerNorm then per-sample modulation, one pass) and modulate.
+//
+// Layout: row-major [rows, cols]. A row belongs to one wave (or to a group of
+// four waves when it is long and rows are few), each lane holding K 16-byte
+// chunks of it in registers, so the row crosses HBM once each way. Chunk k of
+// lane l is chunk (k * W + wave) * 64 + l of the row: every load and store
+// instruction of a wave covers 1 KiB of contiguous memory.
+//
+// Arithmetic is the runner's CPU reference's (ops/CpuNormalisation.scala:53-71,
+// :128-151, ops/CpuElementwise.scala:212-217): sums, factor and every output in
+// double, rounded once to float (then to bf16). CDNA4 runs double at the same
+// vector rate as unpacked float, so this costs no more than float math and
+// the results match the reference to the last bit but for sums taken in
+// another order.
+#include "common.hpp"
+
+namespace drift {
+namespace {
+
+// The sum over a row's group of W waves (W = 1 or 4), the same in every lane.
+template <int W>
+__device__ __forceinline__ double row_sum(double v, double* partial) {
+  v = group_sum<64>(v);
+  if constexpr (W > 1) {
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) partial[wave] = v;
+    __syncthreads();
+    v = partial[0];
+#pragma unroll
+    for (int w = 1; w < W; ++w) v += partial[w];
+    __syncthreads();  // partial is reused by the next sum
+  }
+  return v;
+}
+
+// Four or eight consecutive F32 weights, as the chunk of type T they pair with.
+template <int N>
+__device__ __forceinline__ void load_f32(const float* p, float (&v)[N]) {
+#pragma unroll
+  for (int j = 0; j < N; j += 4) {
+    const float4 q = *reinterpret_cast<const float4*>(p + j);
+    v[j] = q.x;
+    v[j + 1] = q.y;
+    v[j + 2] = q.z;
+    v[j + 3] = q.w;
+  }
+}
+
+// ------------------------------------------------------------------ RMSNorm
+
+template <typename T, int K, int W>
+__global__ void __launch_bounds__(256) rms_norm_rows(T* x, const T* y, const float* weight, T* out, int64_t rows,
+                                                     int cols, float eps, float offset, int weight_rows) {
+  constexpr int N = Chunk<T>::N;
+  constexpr int kRowsPerBlock = 4 / W;
+  __shared__ double partial[4];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int sub = wave % W;
+  const int chunks = cols / N;
+  for (int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + wave / W; row < rows;
+       row += (int64_t)gridDim.x * kRowsPerBlock) {
+    T* xr = x + row * cols;
+    float v[K][N];
+    double squares = 0.0;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const int c = (k * W + sub) * kWave + lane;
+      if (c < chunks) {
+        Chunk<T>::load(xr + c * N, v[k]);
+        if (y) {
+          float u[N];
+          Chunk<T>::load(y + row * cols + c * N, u);
+#pragma unroll
+          for (int j = 0; j < N; ++j) v[k][j] += u[j];  // the F32 sum, as add() rounds it
+        }
+#pragma unroll
+        for (int j = 0; j < N; ++j) squares += (double)v[k][j] * (double)v[k][j];
+      }
+    }
+    squares = row_sum<W>(squares, partial);
+    const double factor = 1.0 / sqrt(squares / (double)cols + (double)eps);
+    const float* w = weight + (row % weight_rows) * cols;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const int c = (k * W + sub) * kWave + lane;
+      if (c < chunks) {
+        if (y) Chunk<T>::store(xr + c * N, v[k]);  // the residual stream, before out (which may be x)
+        float wv[N], o[N];
+        load_f32<N>(w + c * N, wv);
+#pragma unroll
+        for (int j = 0; j < N; ++j) o[j] = (float)((double)v[k][j] * factor * ((double)wv[j] + (double)offset));
+        Chunk<T>::store(out + row * cols + c * N, o);
+      }
+    }
+  }
+}
+
+// Any width and alignment: a block of 256 per row, reading the row twice.
+template <typename T>
+__global__ void __launch_bounds__(256) rms_norm_rows_scalar(T* x, const T* y, const float* weight, T* out,
+                                                            int64_t rows, int cols, float eps, float offset,
+                                                            int weight_rows) {
+  __shared__ double partial[4];
+  for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
+    T* xr = x + row * cols;
+    const T* yr = y ? y + row * cols : nullptr;
+    double squares = 0.0;
+    for (int c = threadIdx.x; c < cols; c += 256) {
+      float v = load_one(xr + c);
+      if (yr) v += load_one(yr + c);
+      squares += (double)v * (double)v;
+    }
+    squares = row_sum<4>(squares, partial);
+    const double factor = 1.0 / sqrt(squares / (double)cols + (double)eps);
+    const float* w = weight + (row % weight_rows) * cols;
+    for (int c = threadIdx.x; c < cols; c += 256) {
+      float v = load_one(xr + c);
+      if (yr) {
+        v += load_one(yr + c);
+        store_one(xr + c, v);
+      }
+      store_one(out + row * cols + c, (float)((double)v * factor * ((double)w[c] + (double)offset)));
+    }
+  }
+}
+
+// ------------------------------------------------------------------ LayerNorm / AdaLN
+
+// MODULATE false: out = normal * (weight or 1) + (bias or 0).
+// MODULATE true: n = float(normal + 0) (layerNorm's F32 result, no affine),
+// out = n * (1 + scale[s, c]) + shift[s, c], s the row's sample.
+template <typename T, int K, int W, bool MODULATE>
+__global__ void __launch_bounds__(256) layer_norm_rows(const T* x, const float* weight, const float* bias, T* out,
+                                                       int64_t rows, int cols, int64_t rows_per_sample, float eps) {
+  constexpr int N = Chunk<T>::N;
+  constexpr int kRowsPerBlock = 4 / W;
+  __shared__ double partial[4];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int sub = wave % W;
+  const int chunks = cols / N;
+  for (int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + wave / W; row < rows;
+       row += (int64_t)gridDim.x * kRowsPerBlock) {
+    float v[K][N];
+    double sum = 0.0;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const int c = (k * W + sub) * kWave + lane;
+      if (c < chunks) {
+        Chunk<T>::load(x + row * cols + c * N, v[k]);
+#pragma unroll
+        for (int j = 0; j < N; ++j) sum += (double)v[k][j];
+      }
+    }
+    const double mean = row_sum<W>(sum, partial) / (double)cols;
+    double squares = 0.0;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const int c = (k * W + sub) * kWave + lane;
+      if (c < chunks) {
+#pragma unroll
+        for (int j = 0; j < N; ++j) {
+          const double d = (double)v[k][j] - mean;
+          squares += d * d;
+        }
+      }
+    }
+    const double factor = 1.0 / sqrt(row_sum<W>(squares, partial) / (double)cols + (double)eps);
+    const float* s0 = weight;  // MODULATE: the sample's scale row
+    const float* s1 = bias;    // MODULATE: the sample's shift row
+    if constexpr (MODULATE) {
+      const int64_t sample = row / rows_per_sample;
+      s0 = weight + sample * cols;
+      s1 = bias + sample * cols;
+    }
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const int c = (k * W + sub) * kWave + lane;
+      if (c < chunks) {
+        float o[N];
+        if constexpr (MODULATE) {
+          float sc[N], sh[N];
+          load_f32<N>(s0 + c * N, sc);
+          load_f32<N>(s1 + c * N, sh);
+#pragma unroll
+          for (int j = 0; j < N; ++j) {
+            const float n = (float)fma((double)v[k][j] - mean, factor, 0.0);
+            o[j] = (float)fma((double)n, 1.0 + (double)sc[j], (double)sh[j]);
+          }
+        } else {
+          float wv[N], bv[N];
+          if (s0) load_f32<N>(s0 + c * N, wv);
+          if (s1) load_f32<N>(s1 + c * N, bv);
+#pragma unroll
+          for (int j = 0; j < N; ++j) {
+            const double normal = ((double)v[k][j] - mean) * factor;
+            o[j] = (float)(normal * (s0 ? (double)wv[j] : 1.0) + (s1 ? (double)bv[j] : 0.0));
+          }
+        }
+        Chunk<T>::store(out + row * cols + c * N, o);
+      }
+    }
+  }
+}
+
+template <typename T, bool MODULATE>
+__global__ void __launch_bounds__(256) layer_norm_rows_scalar(const T* x, const float* weight, const float* bias,
+                                                              T* out, int64_t rows, int cols,
+                                                              int64_t rows_per_sample, float eps) {
+  __shared__ double partial[4];
+  for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
+    const T* xr = x + row * cols;
+    double sum = 0.0;
+    for (int c = threadIdx.x; c < cols; c += 256) sum += (double)load_one(xr + c);
+    const double mean = row_sum<4>(sum, partial) / (double)cols;
+    double squares = 0.0;
+    for (int c = threadIdx.x; c < cols; c += 256) {
+      const double d = (double)load_one(xr + c) - mean;
+      squares += d * d;
+    }
+    const double factor = 1.0 / sqrt(row_sum<4>(squares, partial) / (double)cols + (double)eps);
+    const float* s0 = weight;
+    const float* s1 = bias;
+    if constexpr (MODULATE) {
+      const int64_t sample = row / rows_per_sample;
+      s0 = weight + sample * cols;
+      s1 = bias + sample * cols;
+    }
+    for (int c = threadIdx.x; c < cols; c += 256) {
+      const double d = (double)load_one(xr + c) - mean;
+      float o;
+      if constexpr (MODULATE) {
+        const float n = (float)fma(d, factor, 0.0);
+        o = (float)fma((double)n, 1.0 + (double)s0[c], (double)s1[c]);
+      } else {
+        o = (float)(d * factor * (s0 ? (double)s0[c] : 1.0) + (s1 ? (double)s1[c] : 0.0));
+      }
+      store_one(out + row * cols + c, o);
+    }
+  }
+}
+
+// ------------------------------------------------------------------ modulate
+
+template <typename T>
+__global__ void __launch_bounds__(256) modulate_elements(const T* x, const float* scale, const float* shift, T* out,
+                                                         int64_t n, int cols) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const int c = (int)(i % cols);
+    store_one(out + i, (float)fma((double)load_one(x + i), 1.0 + (double)scale[c], (double)shift[c]));
+  }
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256) modulate_chunks(const T* x, const float* scale, const float* shift, T* out,
+                                                       int64_t chunks, int cols) {
+  constexpr int N = Chunk<T>::N;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < chunks; i += stride) {
+    const int c = (int)((i * N) % cols);
+    float v[N], sc[N], sh[N], o[N];
+    Chunk<T>::load(x + i * N, v);
+    load_f32<N>(scale + c, sc);
+    load_f32<N>(shift + c, sh);
+#pragma unroll
+    for (int j = 0; j < N; ++j) o[j] = (float)fma((double)v[j], 1.0 + (double)sc[j], (double)sh[j]);
+    Chunk<T>::store(out + i * N, o);
+  }
+}
+
+// ------------------------------------------------------------------ launch layer
+
+// How a row is split: W waves per row, K chunks per lane; K = 0 means the
+// scalar path.
+struct RowPlan {
+  int waves = 1;
+  int per_lane = 0;
+};
+
+template <typename T>
+RowPlan plan_rows(int64_t rows, int cols, bool vector_ok) {
+  constexpr int N = Chunk<T>::N;
+  RowPlan plan;
+  if (!vector_ok || cols % N != 0) return plan;
+  const int chunks = cols / N;
+  // few long rows: a 4-wave group per row shortens each lane's chain
+  plan.waves = (chunks > kWave * 16 || (rows < 1024 && chunks >= 4 * kWave)) ? 4 : 1;
+  const int per_lane = (int)ceil_div(chunks, kWave * plan.waves);
+  static const int kSteps[] = {1, 2, 3, 4, 6, 8, 12, 16};
+  for (int k : kSteps)
+    if (per_lane <= k) {
+      plan.per_lane = k;
+      break;
+    }
+  return plan;
+}
+
+#define DRIFT_ROW_CASES(MACRO) \
+  MACRO(1)                     \
+  MACRO(2)                     \
+  MACRO(3)                     \
+  MACRO(4)                     \
+  MACRO(6)                     \
+  MACRO(8)                     \
+  MACRO(12)                    \
+  MACRO(16)
+
+template <typename T>
+int rms_norm(const char* entry, T* x, const T* y, const float* weight, T* out, int64_t rows, int32_t cols, float eps,
+             float offset, int32_t weight_rows, void* stream) {
+  clear_error();
+  if (rows < 0) return refuse("%s: %lld rows", entry, (long long)rows);
+  if (cols <= 0) return refuse("%s: rows of %d values", entry, cols);
+  if (weight_rows <= 0) return refuse("%s: %d weight rows", entry, weight_rows);
+  if (rows == 0) return 0;
+  if (!x || !weight || !out) return refuse("%s: null x, weight or out", entry);
+  const hipStream_t s = (hipStream_t)stream;
+  const bool vector_ok = aligned16(x) && aligned16(out) && aligned16(weight) && (!y || aligned16(y));
+  const RowPlan plan = plan_rows<T>(rows, cols, vector_ok);
+  if (plan.per_lane == 0) {
+    hipLaunchKernelGGL(rms_norm_rows_scalar<T>, dim3(grid_for(rows, 1)), dim3(256), 0, s, x, y, weight, out, rows,
+                       (int)cols, eps, offset, (int)weight_rows);
+    return launched(entry);
+  }
+  const unsigned grid = grid_for(rows, 4 / plan.waves);
+#define DRIFT_RMS_CASE(K)                                                                                       \
+  case K:                                                                                                       \
+    if (plan.waves == 1)                                                                                        \
+      hipLaunchKernelGGL((rms_norm_rows<T, K, 1>), dim3(grid), dim3(256), 0, s, x, y, weight, out, rows, cols, \
+                         eps, offset, weight_rows);                                                             \
+    else                                                                                                        \
+      hipLaunchKernelGGL((rms_norm_rows<T, K, 4>), dim3(grid), dim3(256), 0, s, x, y, weight, out, rows, cols, \
+                         eps, offset, weight_rows);                                                             \
+    break;
+  switch (plan.per_lane) { DRIFT_ROW_CASES(DRIFT_RMS_CASE) }
+#undef DRIFT_RMS_CASE
+  return launched(entry);
+}
+
+template <typename T, bool MODULATE>
+int layer_norm(const char* entry, const T* x, const float* weight, const float* bias, T* out, int64_t rows,
+               int32_t cols, int64_t rows_per_sample, float eps, void* stream) {
+  clear_error();
+  if (rows < 0) return refuse("%s: %lld rows", entry, (long long)rows);
+  if (cols <= 0) return refuse("%s: rows of %d values", entry, cols);
+  if (MODULATE && rows_per_sample <= 0) return refuse("%s: %lld rows per sample", entry, (long long)rows_per_sample);
+  if (rows == 0) return 0;
+  if (!x || !out) return refuse("%s: null x or out", entry);
+  if (MODULATE && (!weight || !bias)) return refuse("%s: null scale or shift", entry);
+  const hipStream_t s = (hipStream_t)stream;
+  const bool vector_ok =
+      aligned16(x) && aligned16(out) && (!weight || aligned16(weight)) && (!bias || aligned16(bias));
+  const RowPlan plan = plan_rows<T>(rows, cols, vector_ok);
+  if (plan.per_lane == 0) {
+    hipLaunchKernelGGL((layer_norm_rows_scalar<T, MODULATE>), dim3(grid_for(rows, 1)), dim3(256), 0, s, x, weight,
+                       bias, out, rows, (int)cols, rows_per_sample, eps);
+    return launched(entry);
+  }
+  const unsigned grid = grid_for(rows, 4 / plan.waves);
+#define DRIFT_LN_CASE(K)                                                                                     \
+  case K:                                                                                                    \
+    if (plan.waves == 1)                                                                                     \
+      hipLaunchKernelGGL((layer_norm_rows<T, K, 1, MODULATE>), dim3(grid), dim3(256), 0, s, x, weight, bias, \
+                         out, rows, cols, rows_per_sample, eps);                                             \
+    else                                                                                                     \
+      hipLaunchKernelGGL((layer_norm_rows<T, K, 4, MODULATE>), dim3(grid), dim3(256), 0, s, x, weight, bias, \
+                         out, rows, cols, rows_per_sample, eps);                                             \
+    break;
+  switch (plan.per_lane) { DRIFT_ROW_CASES(DRIFT_LN_CASE) }
+#undef DRIFT_LN_CASE
+  return launched(entry);
+}
+
+}  // namespace
+}  // namespace drift
+
+using namespace drift;
+
+extern "C" int drift_rms_norm_f32(float* x, const float* y, const float* weight, float* out, int64_t rows,
+                                  int32_t cols, float eps, float offset, int32_t weight_rows, void* stream) {
+  return rms_norm<float>("drift_rms_norm_f32", x, y, weight, out, rows, cols, eps, offset, weight_rows, stream);
+}
+
+extern "C" int drift_rms_norm_bf16(uint16_t* x, const uint16_t* y, const float* weight, uint16_t* out,
+                                   int64_t rows, int32_t cols, float eps, float offset, int32_t weight_rows,
+                                   void* stream) {
+  return rms_norm<uint16_t>("drift_rms_norm_bf16", x, y, weight, out, rows, cols, eps, offset, weight_rows, stream);
+}
+
+extern "C" int drift_layer_norm_f32(const float* x, const float* weight, const float* bias, float* out,
+                                    int64_t rows, int32_t cols, float eps, void* stream) {
+  return layer_norm<float, false>("drift_layer_norm_f32", x, weight, bias, out, rows, cols, 1, eps, stream);
+}
+
+extern "C" int drift_layer_norm_modulate_f32(const float* x, const float* scale, const float* shift, float* out,
+                                             int64_t rows, int32_t cols, int64_t rows_per_sample, float eps,
+                                             void* stream) {
+  return layer_norm<float, true>("drift_layer_norm_modulate_f32", x, scale, shift, out, rows, cols,
+                                 rows_per_sample, eps, stream);
+}
+
+extern "C" int drift_layer_norm_modulate_bf16(const uint16_t* x, const float* scale, const float* shift,
+                                              uint16_t* out, int64_t rows, int32_t cols, int64_t rows_per_sample,
+                                              float eps, void* stream) {
+  return layer_norm<uint16_t, true>("drift_layer_norm_modulate_bf16", x, scale, shift, out, rows, cols,
+                                    rows_per_sample, eps, stream);
+}
+
+extern "C" int drift_modulate_f32(const float* x, const float* scale, const float* shift, float* out, int64_t rows,
+                                  int32_t cols, void* stream) {
+  const char* entry = "drift_modulate_f32";
+  clear_error();
+  if (rows < 0) return refuse("%s: %lld rows", entry, (long long)rows);
+  if (cols <= 0) return refuse("%s: rows of %d values", entry, cols);
+  if (rows == 0) return 0;
+  if (!x || !scale || !shift || !out) return refuse("%s: null x, scale, shift or out", entry);
+  const hipStream_t s = (hipStream_t)stream;
+  const int64_t n = rows * cols;
+  if (cols % 4 == 0 && aligned16(x) && aligned16(out) && aligned16(scale) && aligned16(shift)) {
+    const int64_t chunks = n / 4;
+    hipLaunchKernelGGL(modulate_chunks<float>, dim3(grid_for(chunks, 256)), dim3(256), 0, s, x, scale, shift, out,
+                       chunks, (int)cols);
+  } else {
+    hipLaunchKernelGGL(modulate_elements<float>, dim3(grid_for(n, 256)), dim3(256), 0, s, x, scale, shift, out, n,
+                       (int)cols);
+  }
+  return launched(entry);
+}

@@ -1,0 +1,399 @@
+"""`HipOps`: the drift runner's operation interface for the fused layer
+kernels' path, over libdrift_kernels.
+
+It mirrors the runner's Scala `Ops` trait (runner/src/drift/runner/ops/Ops.scala:15-34)
+for the methods on this path: same names, same argument meaning, and the
+same shape and dtype rules, checked before any launch and refused with a
+`ValueError` carrying the reference's message (the reference throws
+IllegalArgumentException from `require`, ops/Ops.scala:36-93). Tensors are
+torch tensors in device memory; `out` is written, never read, and may be an
+input of the elementwise and row-wise operations.
+
+Beyond the reference's F32 activations, the kernels take BF16 tensors
+(torch.bfloat16) with F32 norm, modulation and rope vectors: the reference's
+bf16 path is convert -> F32 op -> convert, which these produce in one pass.
+Everything launches asynchronously on the current torch stream (or the
+stream given to the constructor); nothing synchronizes.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import enum
+from dataclasses import dataclass
+from typing import Optional, Sequence
+
+import torch
+
+from . import _lib
+
+F32, BF16, F16, I32 = torch.float32, torch.bfloat16, torch.float16, torch.int32
+_FLOAT_TYPES = (F32, BF16)
+
+
+class Activation(enum.IntEnum):
+    """ops/Activation.scala:6-20; the value is the kernels' `kind`."""
+    Silu = 0
+    GeluTanh = 1
+    GeluErf = 2
+    Sigmoid = 3
+    Situ = 4
+
+
+class RopeLayout(enum.IntEnum):
+    """ops/Rope.scala:7-12."""
+    Neox = 0
+    Interleaved = 1
+
+
+@dataclass(frozen=True)
+class RopeSections:
+    """ops/Rope.scala:14-37: which position each pair turns by."""
+    code: int
+    sizes: tuple = ()
+
+    @staticmethod
+    def Single() -> "RopeSections":
+        return RopeSections(0)
+
+    @staticmethod
+    def Contiguous(temporal: int, height: int, width: int) -> "RopeSections":
+        return RopeSections(1, (temporal, height, width))
+
+    @staticmethod
+    def Interleaved(temporal: int, height: int, width: int) -> "RopeSections":
+        return RopeSections(2, (temporal, height, width))
+
+    @staticmethod
+    def Axes(pairs: Sequence[int]) -> "RopeSections":
+        return RopeSections(3, tuple(pairs))
+
+    @property
+    def positionsPerToken(self) -> int:
+        return 1 if self.code == 0 else (len(self.sizes) if self.code == 3 else 3)
+
+    def launch_sizes(self) -> tuple:
+        """`rope_f32`'s four section sizes (ops/HipAttention.scala:73-79)."""
+        return tuple(self.sizes) + (0,) * (4 - len(self.sizes))
+
+
+@dataclass(frozen=True)
+class Rope:
+    """ops/Rope.scala:39-46."""
+    theta: float
+    rotaryDimensions: int
+    layout: RopeLayout = RopeLayout.Neox
+    sections: RopeSections = RopeSections(0)
+
+
+@dataclass
+class RowNorm:
+    """ops/RowNorm.scala:17-23: an RMS norm taken of a result as it is written."""
+    weight: torch.Tensor
+    epsilon: float
+    weightOffset: float
+    out: torch.Tensor
+
+
+@dataclass
+class QueryKeyNorms:
+    """ops/RowNorm.scala:5-15: query and key RMS norms, then `rope`."""
+    queryNorm: torch.Tensor
+    keyNorm: torch.Tensor
+    epsilon: float
+    weightOffset: float
+    rope: Rope
+
+
+@dataclass
+class Q8_0Table:
+    """A Q8_0 table ([vocabulary, cols] values) as its bytes: a uint8 tensor
+    [vocabulary, cols / 32 * 34], per 32 values an fp16 scale then 32 int8
+    codes (tensor/GgmlQuants.scala:104-118)."""
+    data: torch.Tensor
+    cols: int
+
+    @property
+    def shape(self) -> tuple:
+        return (self.data.shape[0], self.cols)
+
+
+# ------------------------------------------------------------------ checks
+# object Ops (ops/Ops.scala:36-93) and the groups' checks.
+
+def _require(condition: bool, message: str) -> None:
+    if not condition:
+        raise ValueError(message)
+
+
+def _name(dtype) -> str:
+    return {F32: "F32", BF16: "BF16", F16: "F16", I32: "I32"}.get(dtype, str(dtype))
+
+
+def _shape(t) -> str:
+    return "[" + ", ".join(str(d) for d in t.shape) + "]"
+
+
+def requireF32(operation: str, *tensors) -> None:
+    for t in tensors:
+        _require(t.dtype == F32, f"{operation} takes F32, not {_name(t.dtype)}")
+
+
+def requireSameShape(operation: str, *tensors) -> None:
+    _require(len({tuple(t.shape) for t in tensors}) == 1,
+             f"{operation} needs equal shapes, got {', '.join(_shape(t) for t in tensors)}")
+
+
+def checkElementwise(operation: str, *tensors) -> None:
+    """Same-shape operands of one float type (F32, or BF16 here)."""
+    _require(tensors[0].dtype in _FLOAT_TYPES, f"{operation} takes F32 or BF16, not {_name(tensors[0].dtype)}")
+    for t in tensors[1:]:
+        _require(t.dtype == tensors[0].dtype,
+                 f"{operation} takes one type, not {_name(tensors[0].dtype)} and {_name(t.dtype)}")
+    requireSameShape(operation, *tensors)
+
+
+def checkRowWise(operation: str, x, out, *rowVectors) -> int:
+    """Returns the row count (ops/Ops.scala:76-92)."""
+    checkElementwise(operation, x, out)
+    _require(x.dim() >= 1, f"{operation} needs at least one dimension")
+    for vector in rowVectors:
+        requireF32(operation, vector)
+        _require(tuple(vector.shape) == (x.shape[-1],), f"{operation}: {_shape(vector)} for rows of {x.shape[-1]}")
+    return x.numel() // x.shape[-1] if x.shape[-1] else 0
+
+
+def checkRope(x, positions, rope: Rope, out) -> tuple:
+    """ops/AttentionOps.scala:185-223; returns (tokens, heads, headDimension)."""
+    checkElementwise("rope", x, out)
+    _require(x.dim() == 3, f"rope takes [tokens, heads, headDimension], got {_shape(x)}")
+    tokens, heads, dimension = x.shape
+    _require(positions.dtype == I32, f"rope positions are I32, not {_name(positions.dtype)}")
+    if rope.sections.code == 3:
+        pairs = rope.sections.sizes
+        _require(len(pairs) <= 4 and all(p > 0 for p in pairs) and sum(pairs) * 2 == rope.rotaryDimensions,
+                 f"rope: axes of {list(pairs)} pairs for {rope.rotaryDimensions} rotary values")
+    count = rope.sections.positionsPerToken
+    expected = (tokens,) if count == 1 else (count, tokens)
+    _require(tuple(positions.shape) == expected,
+             f"rope positions {_shape(positions)}, expected [{', '.join(map(str, expected))}]")
+    _require(rope.rotaryDimensions % 2 == 0 and rope.rotaryDimensions <= dimension,
+             f"rope: {rope.rotaryDimensions} rotary dimensions in heads of {dimension}")
+    return tokens, heads, dimension
+
+
+def checkRopeTable(x, cosines, sines, out) -> tuple:
+    """ops/AttentionOps.scala:129-151; returns (tokens, heads, D, pairs, perHead)."""
+    checkElementwise("ropeTable", x, out)
+    requireF32("ropeTable", cosines, sines)
+    _require(x.dim() == 3, f"ropeTable takes [tokens, heads, D], not {_shape(x)}")
+    tokens, heads, d = x.shape
+    pairs = cosines.shape[-1]
+    per_head = cosines.dim() == 3
+    _require((tuple(cosines.shape) in ((tokens, pairs), (tokens, heads, pairs)))
+             and sines.shape == cosines.shape and 2 * pairs <= d,
+             f"ropeTable: tables {_shape(cosines)}, {_shape(sines)} for {_shape(x)}")
+    return tokens, heads, d, pairs, per_head
+
+
+def checkEmbedding(table, ids, out) -> None:
+    """ops/LinearOps.scala:92-106."""
+    shape = table.shape
+    _require(len(shape) == 2, f"an embedding table is [vocabulary, D], not {list(shape)}")
+    _require(ids.dtype == I32 and ids.dim() == 1,
+             f"embedding ids are I32 [tokens], not {_name(ids.dtype)} {_shape(ids)}")
+    _require(out.dtype in _FLOAT_TYPES, f"embedding takes F32 or BF16, not {_name(out.dtype)}")
+    _require(tuple(out.shape) == (ids.shape[0], shape[-1]),
+             f"embedding: out {_shape(out)} for {ids.shape[0]} rows of {shape[-1]}")
+
+
+_CONVERSIONS = {(F32, BF16): 0, (BF16, F32): 1, (F32, F16): 2, (F16, F32): 3}
+
+
+def checkConvert(x, out) -> int:
+    """ops/MemoryOps.scala:68-84, for the float types."""
+    requireSameShape("convert", x, out)
+    kind = _CONVERSIONS.get((x.dtype, out.dtype))
+    _require(kind is not None, f"convert: no conversion from {_name(x.dtype)} to {_name(out.dtype)}")
+    return kind
+
+
+def _on_device(operation: str, *tensors) -> None:
+    for t in tensors:
+        _require(t.is_cuda, f"{operation}: tensors live in device memory")
+        _require(t.is_contiguous(), f"{operation}: tensors are dense row-major")
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _suffix(dtype) -> str:
+    return "f32" if dtype == F32 else "bf16"
+
+
+# ------------------------------------------------------------------ the backend
+
+class HipOps:
+    """The GPU backend of this path (the reference's HipOps, ops/HipOps.scala),
+    launching libdrift_kernels on `stream` (default: torch's current stream)."""
+
+    name = "hip"
+
+    def __init__(self, stream: Optional[torch.cuda.Stream] = None):
+        _lib.load()
+        self.stream = stream
+        self.onWork = lambda: None  # ops/Ops.scala:29-33
+
+    def _stream(self):
+        s = self.stream if self.stream is not None else torch.cuda.current_stream()
+        return ctypes.c_void_p(s.cuda_stream)
+
+    def _launch(self, entry: str, *args) -> None:
+        self.onWork()
+        _lib.call(entry, *args, self._stream())
+
+    # ---------------------------------------------------------------- norms
+
+    def rmsNorm(self, x, weight, epsilon: float, weightOffset: float, out) -> None:
+        """`out = x / sqrt(mean(x^2) + epsilon) * (weight + weightOffset)`
+        (ops/NormalisationOps.scala:30-45)."""
+        rows = checkRowWise("rmsNorm", x, out, weight)
+        _on_device("rmsNorm", x, weight, out)
+        self._launch(f"drift_rms_norm_{_suffix(x.dtype)}", _ptr(x), None, _ptr(weight), _ptr(out), rows,
+                     x.shape[-1], epsilon, weightOffset, 1)
+
+    def addRmsNorm(self, x, y, norm: RowNorm) -> None:
+        """`x += y`, then `norm`'s RMS norm of x into its out, in one launch
+        (ops/NormalisationOps.scala:131-138, ops/HipNormalisation.scala:117-131)."""
+        checkElementwise("addRmsNorm", x, y)
+        rows = checkRowWise("addRmsNorm", x, norm.out, norm.weight)
+        _on_device("addRmsNorm", x, y, norm.weight, norm.out)
+        self._launch(f"drift_rms_norm_{_suffix(x.dtype)}", _ptr(x), _ptr(y), _ptr(norm.weight), _ptr(norm.out),
+                     rows, x.shape[-1], norm.epsilon, norm.weightOffset, 1)
+
+    def layerNorm(self, x, weight: Optional[torch.Tensor], bias: Optional[torch.Tensor], epsilon: float,
+                  out) -> None:
+        """ops/NormalisationOps.scala:74-80 (F32, as the reference's kernel)."""
+        rows = checkRowWise("layerNorm", x, out, *[t for t in (weight, bias) if t is not None])
+        requireF32("layerNorm", x)
+        _on_device("layerNorm", x, out, *[t for t in (weight, bias) if t is not None])
+        self._launch("drift_layer_norm_f32", _ptr(x), _ptr(weight), _ptr(bias), _ptr(out), rows, x.shape[-1],
+                     epsilon)
+
+    def modulate(self, x, scale, shift, out) -> None:
+        """`out = x * (1 + scale) + shift` (ops/ElementwiseOps.scala:28), F32."""
+        rows = checkRowWise("modulate", x, out, scale, shift)
+        requireF32("modulate", x)
+        _on_device("modulate", x, scale, shift, out)
+        self._launch("drift_modulate_f32", _ptr(x), _ptr(scale), _ptr(shift), _ptr(out), rows, x.shape[-1])
+
+    def layerNormModulate(self, x, scale, shift, epsilon: float, out, rowsPerSample: Optional[int] = None) -> None:
+        """AdaLN in one launch: layerNorm(x, None, None, epsilon) then
+        modulate with sample s's row of `scale` and `shift` ([samples, C])
+        over that sample's rows (models/Wan.scala:431-432). x, out [rows, C]."""
+        checkElementwise("layerNormModulate", x, out)
+        requireF32("layerNormModulate", scale, shift)
+        _require(x.dim() == 2, f"layerNormModulate takes [rows, C], not {_shape(x)}")
+        rows, cols = x.shape
+        scale2 = scale.reshape(-1, cols) if scale.dim() == 1 else scale
+        _require(scale2.dim() == 2 and scale2.shape[1] == cols and tuple(shift.shape) == tuple(scale.shape),
+                 f"layerNormModulate: scale {_shape(scale)}, shift {_shape(shift)} for rows of {cols}")
+        samples = scale2.shape[0]
+        per = rowsPerSample if rowsPerSample is not None else -(-rows // samples)
+        _require(per > 0 and samples * per >= rows,
+                 f"layerNormModulate: {samples} samples of {per} rows for {rows} rows")
+        _on_device("layerNormModulate", x, scale, shift, out)
+        self._launch(f"drift_layer_norm_modulate_{_suffix(x.dtype)}", _ptr(x), _ptr(scale), _ptr(shift), _ptr(out),
+                     rows, cols, per, epsilon)
+
+    # ---------------------------------------------------------------- activations
+
+    def activation(self, kind: Activation, x, out) -> None:
+        self.scaledActivation(kind, 1.0, x, out)
+
+    def scaledActivation(self, kind: Activation, inputScale: float, x, out) -> None:
+        """`out = kind(inputScale * x)` (ops/NormalisationOps.scala:10-19)."""
+        checkElementwise("activation", x, out)
+        _on_device("activation", x, out)
+        self._launch(f"drift_activation_{_suffix(x.dtype)}", _ptr(x), _ptr(out), x.numel(), int(kind), inputScale)
+
+    def gated(self, kind: Activation, gate, up, out) -> None:
+        """`out = kind(gate) * up` (ops/NormalisationOps.scala:21-24)."""
+        checkElementwise("gated", gate, up, out)
+        _on_device("gated", gate, up, out)
+        self._launch(f"drift_gated_{_suffix(gate.dtype)}", _ptr(gate), _ptr(up), _ptr(out), gate.numel(), int(kind))
+
+    # ---------------------------------------------------------------- rotary
+
+    def rope(self, x, positions, rope: Rope, out) -> None:
+        """ops/AttentionOps.scala:42-45."""
+        tokens, heads, dimension = checkRope(x, positions, rope, out)
+        _on_device("rope", x, positions, out)
+        s = rope.sections.launch_sizes()
+        self._launch(f"drift_rope_{_suffix(x.dtype)}", _ptr(x), _ptr(positions), _ptr(out), tokens, heads, dimension,
+                     rope.rotaryDimensions, rope.theta, int(rope.layout), rope.sections.code, *s)
+
+    def ropeTable(self, x, cosines, sines, out, halves: bool = False) -> None:
+        """ops/AttentionOps.scala:25-40."""
+        tokens, heads, d, pairs, per_head = checkRopeTable(x, cosines, sines, out)
+        _on_device("ropeTable", x, cosines, sines, out)
+        self._launch(f"drift_rope_table_{_suffix(x.dtype)}", _ptr(x), _ptr(cosines), _ptr(sines), _ptr(out), tokens,
+                     heads, d, pairs, int(per_head), int(halves))
+
+    def rope3d(self, x, frames: int, rows: int, columns: int, out, tokenOffset: int = 0,
+               theta: float = 10000.0) -> None:
+        """Wan's 3-D RoPE with the angles made in the kernel: what
+        models/Wan.scala:324-361 tabulates and :442-443 applies, for a
+        `frames x rows x columns` grid; token i of x is grid token
+        (tokenOffset + i) mod (frames * rows * columns)."""
+        checkElementwise("rope3d", x, out)
+        _require(x.dim() == 3, f"rope3d takes [tokens, heads, D], not {_shape(x)}")
+        _on_device("rope3d", x, out)
+        tokens, heads, d = x.shape
+        self._launch(f"drift_rope_3d_{_suffix(x.dtype)}", _ptr(x), _ptr(out), tokens, heads, d, frames, rows,
+                     columns, tokenOffset, theta)
+
+    def queryKeyNormRope(self, q, k, norms: QueryKeyNorms, positions, rotatedQueries, rotatedKeys) -> None:
+        """Per-head RMS norms of queries and keys, then their rope, in one
+        launch: the composition ops/AttentionOps.scala:87-107 runs as
+        rmsNorm, rmsNorm, rope, rope. q [t, heads, D], k [t, kvHeads, D]."""
+        checkElementwise("queryKeyNormRope", q, rotatedQueries)
+        checkElementwise("queryKeyNormRope", k, rotatedKeys)
+        _require(q.dtype == k.dtype, "queryKeyNormRope takes one type for queries and keys")
+        _require(q.dim() == 3 and k.dim() == 3 and q.shape[0] == k.shape[0] and q.shape[2] == k.shape[2],
+                 f"queryKeyNormRope: queries {_shape(q)}, keys {_shape(k)}")
+        tokens, heads, d = q.shape
+        kv = k.shape[1]
+        checkRope(q, positions, norms.rope, rotatedQueries)
+        for name, w in (("queryNorm", norms.queryNorm), ("keyNorm", norms.keyNorm)):
+            requireF32("queryKeyNormRope", w)
+            _require(tuple(w.shape) == (d,), f"queryKeyNormRope: {name} {_shape(w)} for heads of {d}")
+        _on_device("queryKeyNormRope", q, k, rotatedQueries, rotatedKeys, norms.queryNorm, norms.keyNorm, positions)
+        r = norms.rope
+        self._launch(f"drift_qk_norm_rope_{_suffix(q.dtype)}", _ptr(q), _ptr(k), _ptr(rotatedQueries),
+                     _ptr(rotatedKeys), _ptr(norms.queryNorm), _ptr(norms.keyNorm), _ptr(positions), tokens, heads,
+                     kv, d, norms.epsilon, norms.weightOffset, r.rotaryDimensions, r.theta, int(r.layout),
+                     r.sections.code, *r.sections.launch_sizes())
+
+    # ---------------------------------------------------------------- embedding, convert
+
+    def embedding(self, table: Q8_0Table, ids, out, badId: Optional[torch.Tensor] = None) -> None:
+        """Rows `ids` of a Q8_0 table, decoded (ops/LinearOps.scala:16). An id
+        outside the table (which the reference refuses) gets a zero row and
+        sets `badId` (int32 [1], device) to 1 when given."""
+        checkEmbedding(table, ids, out)
+        _require(isinstance(table, Q8_0Table), "embedding: only Q8_0 tables have kernels here")
+        vocab, cols = table.shape
+        _require(cols % 32 == 0, f"{cols} elements are not whole Q8_0 blocks of 32")
+        _require(tuple(table.data.shape) == (vocab, cols // 32 * 34) and table.data.dtype == torch.uint8,
+                 f"embedding: Q8_0 bytes {_shape(table.data)} for rows of {cols}")
+        _on_device("embedding", table.data, ids, out)
+        self._launch(f"drift_embedding_q8_0_{_suffix(out.dtype)}", _ptr(table.data), _ptr(ids), _ptr(out),
+                     ids.shape[0], vocab, cols, _ptr(badId))
+
+    def convert(self, x, out) -> None:
+        """ops/MemoryOps.scala:46."""
+        kind = checkConvert(x, out)
+        _on_device("convert", x, out)
+        self._launch("drift_convert", _ptr(x), _ptr(out), x.numel(), kind)

@@ -1,0 +1,215 @@
+/*
+ * libdrift_kernels: the drift runner's fused layer kernels for MI355X
+ * (gfx950, CDNA4, wave64), behind a plain C ABI.
+ *
+ * Every entry point
+ *   - takes device pointers and sizes, and the HIP stream to launch on
+ *     (`stream` is a hipStream_t; NULL is the default stream);
+ *   - validates its arguments on the host before launching and returns
+ *     hipErrorInvalidValue (1) for bad geometry, with the reason in
+ *     drift_last_error();
+ *   - launches asynchronously: it never synchronizes and never allocates;
+ *   - returns 0 (hipSuccess) or the HIP error of the launch. It never aborts.
+ *
+ * Element types: F32 is float; BF16 is uint16_t holding the top half of an
+ * F32, rounded to nearest even from float results (NaN keeps its top half with
+ * the quiet bit set), as the runner's CpuOps.toBfloat16
+ * (runner/src/drift/runner/ops/CpuOps.scala:426-431). Norm, modulation and
+ * rope vectors are F32; positions and ids are int32.
+ *
+ * Arithmetic follows the runner's CPU reference (`CpuOps`): statistics,
+ * normalisation, modulation and rotations in double (full rate on CDNA4),
+ * activations in float through forms that keep their relative accuracy.
+ *
+ * Aliasing: `out` may be the same buffer as `x` (or `gate`) for every entry
+ * point, rope ones included (each lane reads a pair before it writes it).
+ * Partially overlapping buffers are not supported.
+ *
+ * Each declaration names the reference interface it replaces (paths under
+ * the reference's runner/).
+ */
+#ifndef DRIFT_KERNELS_H
+#define DRIFT_KERNELS_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DRIFT_ABI_VERSION 1
+
+/* Activation kinds: src/drift/runner/ops/Activation.scala:6-20. */
+enum {
+  DRIFT_SILU = 0,
+  DRIFT_GELU_TANH = 1,
+  DRIFT_GELU_ERF = 2,
+  DRIFT_SIGMOID = 3,
+  DRIFT_SITU = 4
+};
+
+/* RoPE layouts and sections: src/drift/runner/ops/Rope.scala:7-46. */
+enum { DRIFT_ROPE_NEOX = 0, DRIFT_ROPE_INTERLEAVED = 1 };
+enum {
+  DRIFT_SECTIONS_SINGLE = 0,
+  DRIFT_SECTIONS_CONTIGUOUS = 1,
+  DRIFT_SECTIONS_INTERLEAVED = 2,
+  DRIFT_SECTIONS_AXES = 3
+};
+
+/* Conversions: src/drift/runner/ops/HipBase.scala:268-274 (codes of
+ * kernels/elementwise.hip:68-86), restricted to the float types. */
+enum {
+  DRIFT_F32_TO_BF16 = 0,
+  DRIFT_BF16_TO_F32 = 1,
+  DRIFT_F32_TO_F16 = 2,
+  DRIFT_F16_TO_F32 = 3
+};
+
+/* The ABI version this library implements (DRIFT_ABI_VERSION). */
+int drift_abi_version(void);
+/* A HIP error code's text. */
+const char* drift_error_string(int code);
+/* Why the calling thread's last refused call was refused ("" if none). */
+const char* drift_last_error(void);
+
+/* ---------------------------------------------------------------- RMSNorm
+ * out = x / sqrt(mean(x^2) + eps) * (weight[r % weight_rows] + offset), per
+ * row of `cols`. With `y` (nullable), x += y is written back first
+ * (addRmsNorm). weight is F32 [weight_rows, cols].
+ * Replaces kernels/norm.hip:34-41 rms_norm_f32 (int8 side outputs xq/xd/xs
+ * not supported) as launched by src/drift/runner/ops/HipNormalisation.scala:57-131
+ * (rmsNorm, normRows, addRmsNorm); the CPU definition is
+ * ops/CpuNormalisation.scala:53-71. */
+int drift_rms_norm_f32(float* x, const float* y, const float* weight, float* out, int64_t rows, int32_t cols,
+                       float eps, float offset, int32_t weight_rows, void* stream);
+/* BF16 x, y, out; F32 weight. The reference's bf16 path is
+ * convert -> rms_norm_f32 -> convert (kernels/elementwise.hip:68-86). */
+int drift_rms_norm_bf16(uint16_t* x, const uint16_t* y, const float* weight, uint16_t* out, int64_t rows,
+                        int32_t cols, float eps, float offset, int32_t weight_rows, void* stream);
+
+/* ---------------------------------------------------------------- LayerNorm, AdaLN
+ * out = (x - mean) / sqrt(var + eps) * weight + bias; weight, bias nullable.
+ * Replaces kernels/norm.hip:63-80 layer_norm_f32
+ * (ops/HipNormalisation.scala:217-238; CPU ops/CpuNormalisation.scala:128-151). */
+int drift_layer_norm_f32(const float* x, const float* weight, const float* bias, float* out, int64_t rows,
+                         int32_t cols, float eps, void* stream);
+
+/* out = x * (1 + scale[c]) + shift[c]. Replaces kernels/elementwise.hip:97-103
+ * modulate_f32 (ops/HipElementwise.scala:77-89; CPU ops/CpuElementwise.scala:212-217). */
+int drift_modulate_f32(const float* x, const float* scale, const float* shift, float* out, int64_t rows,
+                       int32_t cols, void* stream);
+
+/* AdaLN in one pass: layerNorm without affine (its F32 result), then
+ * modulate with sample s's rows of scale and shift ([samples, cols] F32),
+ * sample s being rows [s * rows_per_sample, (s + 1) * rows_per_sample).
+ * Replaces the pair layerNorm(x, None, None, eps) + modulate(...) that
+ * src/drift/runner/models/Wan.scala:431-432,470-471,482-488 launch one sample
+ * at a time. */
+int drift_layer_norm_modulate_f32(const float* x, const float* scale, const float* shift, float* out,
+                                  int64_t rows, int32_t cols, int64_t rows_per_sample, float eps, void* stream);
+int drift_layer_norm_modulate_bf16(const uint16_t* x, const float* scale, const float* shift, uint16_t* out,
+                                   int64_t rows, int32_t cols, int64_t rows_per_sample, float eps,
+                                   void* stream);
+
+/* ---------------------------------------------------------------- activations
+ * out = kind(scale * x), elementwise over n values. Replaces
+ * kernels/elementwise.hip:31-53 activation_f32 (ops/HipNormalisation.scala:14-30;
+ * CPU ops/CpuNormalisation.scala:11-35). */
+int drift_activation_f32(const float* x, float* out, int64_t n, int32_t kind, float scale, void* stream);
+int drift_activation_bf16(const uint16_t* x, uint16_t* out, int64_t n, int32_t kind, float scale, void* stream);
+
+/* out = kind(gate) * up (SiTU soft-caps up as 25 tanh(up / 25)). Replaces
+ * kernels/elementwise.hip:46-65 gated_f32 without its int8 side outputs
+ * (ops/HipNormalisation.scala:32-47; CPU ops/CpuNormalisation.scala:22-41). */
+int drift_gated_f32(const float* gate, const float* up, float* out, int64_t n, int32_t kind, void* stream);
+int drift_gated_bf16(const uint16_t* gate, const uint16_t* up, uint16_t* out, int64_t n, int32_t kind,
+                     void* stream);
+
+/* ---------------------------------------------------------------- RoPE
+ * x, out [tokens, heads, head_dim]; positions int32 [positions_per_token,
+ * tokens] (1 for SINGLE, 3 for mRoPE, the number of nonzero s for AXES).
+ * Pair i turns by position * theta^(-2i/rotary) (AXES: pair j of an axis of
+ * n pairs by theta^(-j/n)); the inverse frequency is the CPU's: pow in
+ * double, rounded to float, then a float reciprocal; the angle is their
+ * float product; the turn is in double. Values from `rotary` on are copied.
+ * Replaces kernels/rope.hip:6-15 rope_f32 with kernels/rope.h:20-51
+ * (ops/HipAttention.scala:74-104; CPU ops/CpuAttention.scala:89-146; checks
+ * ops/AttentionOps.scala:185-223). */
+int drift_rope_f32(const float* x, const int32_t* positions, float* out, int32_t tokens, int32_t heads,
+                   int32_t head_dim, int32_t rotary, float theta, int32_t layout, int32_t sections, int32_t s0,
+                   int32_t s1, int32_t s2, int32_t s3, void* stream);
+int drift_rope_bf16(const uint16_t* x, const int32_t* positions, uint16_t* out, int32_t tokens, int32_t heads,
+                    int32_t head_dim, int32_t rotary, float theta, int32_t layout, int32_t sections, int32_t s0,
+                    int32_t s1, int32_t s2, int32_t s3, void* stream);
+
+/* RoPE from F32 tables cosines, sines [tokens, pairs] (or [tokens, heads,
+ * pairs] with per_head): adjacent pairs (2m, 2m+1), or with `halves` pairs
+ * (m, m + pairs); values past 2 pairs copied. Replaces
+ * kernels/rope.hip:17-55 rope_table_f32 / rope_table_halves_f32
+ * (ops/HipAttention.scala:45-71; CPU ops/CpuAttention.scala:53-87). */
+int drift_rope_table_f32(const float* x, const float* cosines, const float* sines, float* out, int32_t tokens,
+                         int32_t heads, int32_t head_dim, int32_t pairs, int32_t per_head, int32_t halves,
+                         void* stream);
+int drift_rope_table_bf16(const uint16_t* x, const float* cosines, const float* sines, uint16_t* out,
+                          int32_t tokens, int32_t heads, int32_t head_dim, int32_t pairs, int32_t per_head,
+                          int32_t halves, void* stream);
+
+/* Wan's 3-D RoPE with its angles made in the kernel: token i of x sits at
+ * grid index g = (token_offset + i) mod (frames * grid_rows * grid_cols) of a
+ * frames x grid_rows x grid_cols grid; its pairs split into frame, row and
+ * column pairs (head_dim - 4 floor(head_dim/6), 2 floor(head_dim/6),
+ * 2 floor(head_dim/6) values) turning by axis position /
+ * theta^(2 index / (2 pairs_axis)), the angle in double, cos and sin rounded to
+ * float as the host tables are; adjacent pairs. Replaces the host table build
+ * of src/drift/runner/models/Wan.scala:324-361 plus the ropeTable launches at
+ * :442-443. */
+int drift_rope_3d_f32(const float* x, float* out, int64_t tokens, int32_t heads, int32_t head_dim, int32_t frames,
+                      int32_t grid_rows, int32_t grid_cols, int64_t token_offset, double theta, void* stream);
+int drift_rope_3d_bf16(const uint16_t* x, uint16_t* out, int64_t tokens, int32_t heads, int32_t head_dim,
+                       int32_t frames, int32_t grid_rows, int32_t grid_cols, int64_t token_offset, double theta,
+                       void* stream);
+
+/* Per-head RMSNorm of queries and keys fused with their RoPE: q [tokens,
+ * heads, head_dim], k [tokens, kv_heads, head_dim], each head row normed with
+ * q_weight / k_weight ([head_dim] F32, + offset) as rmsNorm does, the F32
+ * result then turned as rope does. Outputs q_out, k_out like q, k (they may
+ * be q, k). Replaces the composition of ops/AttentionOps.scala:87-107 (rmsNorm
+ * of each head in place, then rope of queries and keys) that
+ * src/drift/runner/models/DenseDecoder.scala:834-855 runs as four launches, and
+ * the norm+rope part of kernels/attention.hip:495-536 attention_inputs. */
+int drift_qk_norm_rope_f32(const float* q, const float* k, float* q_out, float* k_out, const float* q_weight,
+                           const float* k_weight, const int32_t* positions, int32_t tokens, int32_t heads,
+                           int32_t kv_heads, int32_t head_dim, float eps, float offset, int32_t rotary, float theta,
+                           int32_t layout, int32_t sections, int32_t s0, int32_t s1, int32_t s2, int32_t s3,
+                           void* stream);
+int drift_qk_norm_rope_bf16(const uint16_t* q, const uint16_t* k, uint16_t* q_out, uint16_t* k_out,
+                            const float* q_weight, const float* k_weight, const int32_t* positions, int32_t tokens,
+                            int32_t heads, int32_t kv_heads, int32_t head_dim, float eps, float offset,
+                            int32_t rotary, float theta, int32_t layout, int32_t sections, int32_t s0, int32_t s1,
+                            int32_t s2, int32_t s3, void* stream);
+
+/* ---------------------------------------------------------------- embedding
+ * Rows `ids` of a Q8_0 table ([vocab, cols], cols a multiple of 32: per 32
+ * values a 34-byte block, fp16 scale d then 32 int8 codes), decoded as
+ * float(code) * d (exact in F32), into out [count, cols]. An id outside
+ * [0, vocab) gets a row of zeros and, when `bad_id` (device int32, nullable)
+ * is given, sets *bad_id = 1; the CPU reference refuses such an id.
+ * Replaces kernels/matvec.hip:830-839,894-897 gather_q8_0
+ * (ops/HipLinear.scala:21-52; CPU ops/CpuLinear.scala:12-41 with
+ * tensor/GgmlQuants.scala:104-118). BF16 output is bit-exact against
+ * convert(embedding F32). */
+int drift_embedding_q8_0_f32(const uint8_t* table, const int32_t* ids, float* out, int64_t count, int64_t vocab,
+                             int32_t cols, int32_t* bad_id, void* stream);
+int drift_embedding_q8_0_bf16(const uint8_t* table, const int32_t* ids, uint16_t* out, int64_t count,
+                              int64_t vocab, int32_t cols, int32_t* bad_id, void* stream);
+
+/* ---------------------------------------------------------------- convert
+ * Elementwise type conversion of n values (kinds above). Replaces
+ * kernels/elementwise.hip:68-86 convert (CPU ops/CpuMemory.scala:84-109). */
+int drift_convert(const void* x, void* out, int64_t n, int32_t kind, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

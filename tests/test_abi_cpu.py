@@ -1,0 +1,82 @@
+"""The C ABI without a GPU: the library loads, exports every entry point the
+header declares, and refuses bad geometry before it would launch anything
+(each call here fails validation, so nothing reaches the device)."""
+
+import ctypes
+
+import pytest
+
+from drift_amd import _lib
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _lib.load()
+
+
+def test_header_and_library_agree(lib):
+    declared = _lib.header_entry_points()
+    assert len(declared) == len(set(declared)) >= 20
+    assert set(declared) == set(_lib.SIGNATURES), "the ctypes table and the header differ"
+    for name in declared:
+        assert hasattr(lib, name), f"{name} is not exported"
+
+
+def test_version_and_error_text(lib):
+    assert lib.drift_abi_version() == _lib.ABI_VERSION == 1
+    assert lib.drift_error_string(0).decode().lower().startswith("no error")
+    assert lib.drift_error_string(1)
+
+
+NULL = None
+
+
+def refused(lib, name, *args):
+    code = getattr(lib, name)(*args)
+    return code == 1 and lib.drift_last_error().decode()
+
+
+def test_norms_refuse_bad_geometry(lib):
+    p = ctypes.c_void_p(16)  # never dereferenced: validation fails first
+    assert "rows of 0 values" in refused(lib, "drift_rms_norm_f32", p, NULL, p, p, 4, 0, 1e-6, 0.0, 1, NULL)
+    assert "-1 rows" in refused(lib, "drift_rms_norm_bf16", p, NULL, p, p, -1, 8, 1e-6, 0.0, 1, NULL)
+    assert "weight rows" in refused(lib, "drift_rms_norm_f32", p, NULL, p, p, 4, 8, 1e-6, 0.0, 0, NULL)
+    assert "null" in refused(lib, "drift_rms_norm_f32", NULL, NULL, p, p, 4, 8, 1e-6, 0.0, 1, NULL)
+    assert "rows per sample" in refused(lib, "drift_layer_norm_modulate_bf16", p, p, p, p, 4, 8, 0, 1e-6, NULL)
+    assert "null scale or shift" in refused(lib, "drift_layer_norm_modulate_f32", p, NULL, p, p, 4, 8, 2, 1e-6, NULL)
+    # empty input: success, nothing launched
+    assert lib.drift_rms_norm_f32(NULL, NULL, NULL, NULL, 0, 8, 1e-6, 0.0, 1, NULL) == 0
+    assert lib.drift_layer_norm_f32(NULL, NULL, NULL, NULL, 0, 8, 1e-6, NULL) == 0
+
+
+def test_elementwise_refuses_bad_arguments(lib):
+    p = ctypes.c_void_p(16)
+    assert "no activation 5" in refused(lib, "drift_activation_f32", p, p, 10, 5, 1.0, NULL)
+    assert "no activation -1" in refused(lib, "drift_gated_bf16", p, p, p, 10, -1, NULL)
+    assert "no conversion 7" in refused(lib, "drift_convert", p, ctypes.c_void_p(32), 10, 7, NULL)
+    assert "same buffer" in refused(lib, "drift_convert", p, p, 10, 0, NULL)
+    assert lib.drift_activation_bf16(NULL, NULL, 0, 1, 1.0, NULL) == 0
+
+
+def test_rope_refuses_what_checkRope_refuses(lib):
+    p = ctypes.c_void_p(16)
+    args = lambda rotary, sections, s: (p, p, p, 4, 2, 128, rotary, 1e4, 0, sections, *s, NULL)
+    # ops/AttentionOps.scala:201-221: even rotary within the head, axes summing to it
+    assert "rotary" in refused(lib, "drift_rope_f32", *args(127, 0, (0, 0, 0, 0)))
+    assert "rotary" in refused(lib, "drift_rope_f32", *args(130, 0, (0, 0, 0, 0)))
+    assert "axes" in refused(lib, "drift_rope_bf16", *args(128, 3, (16, 24, 23, 0)))
+    assert "axes" in refused(lib, "drift_rope_bf16", *args(128, 3, (32, 0, 32, 0)))
+    assert "no layout" in refused(lib, "drift_rope_f32", p, p, p, 4, 2, 128, 128, 1e4, 2, 0, 0, 0, 0, 0, NULL)
+    assert "heads of 1024" in refused(lib, "drift_rope_f32", p, p, p, 4, 2, 1024, 128, 1e4, 0, 0, 0, 0, 0, 0, NULL)
+    assert "pairs in heads" in refused(lib, "drift_rope_table_f32", p, p, p, p, 4, 2, 128, 65, 0, 0, NULL)
+    assert "grid" in refused(lib, "drift_rope_3d_bf16", p, p, 10, 2, 128, 0, 3, 4, 0, 1e4, NULL)
+    assert "too narrow" in refused(lib, "drift_rope_3d_f32", p, p, 10, 2, 4, 1, 1, 1, 0, 1e4, NULL)
+    assert "key heads" in refused(lib, "drift_qk_norm_rope_bf16", p, p, p, p, p, p, p, 4, 2, -1, 128, 1e-6, 0.0,
+                                  128, 1e6, 0, 0, 0, 0, 0, 0, NULL)
+
+
+def test_embedding_refuses_partial_blocks(lib):
+    p = ctypes.c_void_p(16)
+    assert "whole Q8_0 blocks" in refused(lib, "drift_embedding_q8_0_bf16", p, p, p, 4, 10, 48, NULL, NULL)
+    assert "not 16-byte aligned" in refused(lib, "drift_embedding_q8_0_f32", p, p, ctypes.c_void_p(18), 4, 10, 64,
+                                            NULL, NULL)

@@ -1,0 +1,134 @@
+"""RMSNorm, LayerNorm, modulate and AdaLN on the GPU against the oracle.
+
+Shapes are the reference's awkward ones (SmallOpsTests.scala:22-29,
+HipOpsTests.scala:87-110) plus the decode (C2) and diffusion (C5) widths;
+inputs 3 N(0,1) as SmallOpsTests.scala:50-54 draws them."""
+
+import numpy as np
+import pytest
+import torch
+
+from drift_amd import ops as d
+from oracle import oracle as o
+from tests.helpers import (DEV, assert_bf16, assert_f32, bf16_input, dev_bf16, dev_f32, gaussian, host_bits,
+                           host_f32, step)
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(1, 1), (3, 7), (2, 255), (5, 4097), (17, 2560), (1, 2048), (64, 2560), (3, 64), (9, 3072), (2, 8192),
+          (1, 16384), (2, 20000)]
+
+
+@pytest.fixture(scope="module")
+def hip():
+    return d.HipOps()
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+@pytest.mark.parametrize("offset", [0.0, 1.0])
+def test_rms_norm_f32(hip, shape, offset):
+    step(f"rmsNorm f32 {shape} offset {offset}")
+    x = gaussian(1, shape, 3.0)
+    w = gaussian(2, shape[-1])
+    out = torch.empty(shape, dtype=torch.float32, device=DEV)
+    hip.rmsNorm(dev_f32(x), dev_f32(w), 1e-6, offset, out)
+    assert_f32(o.rms_norm(x, w, 1e-6, offset), host_f32(out), what=f"rmsNorm {shape}")
+
+
+@pytest.mark.parametrize("shape", [(1, 4096), (8, 4096), (64, 4096), (3, 7), (5, 4097), (17, 2560), (2, 16384)])
+def test_rms_norm_bf16(hip, shape):
+    step(f"rmsNorm bf16 {shape}")
+    xb = bf16_input(gaussian(3, shape))
+    w = (1 + 0.1 * gaussian(4, shape[-1])).astype(np.float32)
+    out = torch.empty(shape, dtype=torch.bfloat16, device=DEV)
+    hip.rmsNorm(dev_bf16(xb), dev_f32(w), 1e-5, 0.0, out)
+    assert_bf16(o.rms_norm_bf16(xb, w, 1e-5), host_bits(out), what=f"rmsNorm bf16 {shape}")
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("shape", [(3, 7), (4, 4096), (600, 1024)])
+def test_add_rms_norm(hip, dtype, shape):
+    step(f"addRmsNorm {dtype} {shape}")
+    x, y = gaussian(5, shape), gaussian(6, shape)
+    w = gaussian(7, shape[-1])
+    if dtype == "f32":
+        xd, yd = dev_f32(x), dev_f32(y)
+        out = torch.empty(shape, dtype=torch.float32, device=DEV)
+        hip.addRmsNorm(xd, yd, d.RowNorm(dev_f32(w), 1e-6, 0.0, out))
+        summed, want = o.rms_norm(x, w, 1e-6, 0.0, y=y)
+        assert np.array_equal(host_f32(xd), summed), "x += y is the F32 sum"
+        assert_f32(want, host_f32(out), what="addRmsNorm")
+    else:
+        xb, yb = bf16_input(x), bf16_input(y)
+        xd = dev_bf16(xb)
+        out = torch.empty(shape, dtype=torch.bfloat16, device=DEV)
+        hip.addRmsNorm(xd, dev_bf16(yb), d.RowNorm(dev_f32(w), 1e-6, 0.0, out))
+        summed, want = o.rms_norm_bf16(xb, w, 1e-6, y_bits=yb)
+        assert np.array_equal(host_bits(xd), summed), "x += y rounds the F32 sum to bf16"
+        assert_bf16(want, host_bits(out), what="addRmsNorm bf16")
+
+
+def test_rms_norm_in_place_and_zero_rows(hip):
+    step("rmsNorm in place, zero row")
+    x = gaussian(8, (6, 512))
+    x[2] = 0
+    w = gaussian(9, 512)
+    xd = dev_f32(x)
+    hip.rmsNorm(xd, dev_f32(w), 1e-6, 0.0, xd)
+    got = host_f32(xd)
+    assert_f32(o.rms_norm(x, w, 1e-6), got, what="in place")
+    assert np.all(got[2] == 0)
+
+
+@pytest.mark.parametrize("shape", [(1, 1), (3, 7), (2, 255), (5, 4097), (17, 2560), (1, 2048), (4, 3072)])
+@pytest.mark.parametrize("affine", [(False, False), (True, False), (False, True), (True, True)])
+def test_layer_norm_f32(hip, shape, affine):
+    step(f"layerNorm f32 {shape} {affine}")
+    x = gaussian(1, shape, 3.0)
+    w = gaussian(2, shape[-1], 3.0) if affine[0] else None
+    b = gaussian(3, shape[-1], 3.0) if affine[1] else None
+    out = torch.empty(shape, dtype=torch.float32, device=DEV)
+    hip.layerNorm(dev_f32(x), None if w is None else dev_f32(w), None if b is None else dev_f32(b), 1e-5, out)
+    assert_f32(o.layer_norm(x, w, b, 1e-5), host_f32(out), what=f"layerNorm {shape}")
+
+
+@pytest.mark.parametrize("shape", [(5, 64), (3, 6144), (3, 7), (2, 4097)])
+def test_modulate_f32(hip, shape):
+    # SmallOpsTests.scala:242-256 shapes
+    step(f"modulate f32 {shape}")
+    x = gaussian(1, shape, 3.0)
+    s, sh = gaussian(2, shape[-1], 3.0), gaussian(3, shape[-1], 3.0)
+    out = torch.empty(shape, dtype=torch.float32, device=DEV)
+    hip.modulate(dev_f32(x), dev_f32(s), dev_f32(sh), out)
+    assert_f32(o.modulate(x, s, sh), host_f32(out), what=f"modulate {shape}")
+
+
+@pytest.mark.parametrize("rows,cols,samples", [(2 * 60, 3072, 2), (7, 64, 1), (3 * 17, 1536, 3), (10, 4097, 2),
+                                               (6, 8, 3), (4, 12288, 2)])
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_layer_norm_modulate(hip, rows, cols, samples, dtype):
+    step(f"layerNormModulate {dtype} [{rows}, {cols}] x {samples} samples")
+    per = -(-rows // samples)
+    x = gaussian(11, (rows, cols))
+    s = (0.1 * gaussian(12, (samples, cols))).astype(np.float32)
+    sh = (0.1 * gaussian(13, (samples, cols))).astype(np.float32)
+    if dtype == "f32":
+        out = torch.empty((rows, cols), dtype=torch.float32, device=DEV)
+        hip.layerNormModulate(dev_f32(x), dev_f32(s), dev_f32(sh), 1e-6, out, per)
+        assert_f32(o.layer_norm_modulate(x, s, sh, per, 1e-6), host_f32(out), what="AdaLN f32")
+    else:
+        xb = bf16_input(x)
+        out = torch.empty((rows, cols), dtype=torch.bfloat16, device=DEV)
+        hip.layerNormModulate(dev_bf16(xb), dev_f32(s), dev_f32(sh), 1e-6, out, per)
+        assert_bf16(o.layer_norm_modulate_bf16(xb, s, sh, per, 1e-6), host_bits(out), what="AdaLN bf16")
+
+
+def test_layer_norm_modulate_in_place_bf16(hip):
+    step("layerNormModulate bf16 in place")
+    x = gaussian(14, (8, 3072))
+    s = (0.1 * gaussian(15, (2, 3072))).astype(np.float32)
+    sh = (0.1 * gaussian(16, (2, 3072))).astype(np.float32)
+    xb = bf16_input(x)
+    xd = dev_bf16(xb)
+    hip.layerNormModulate(xd, dev_f32(s), dev_f32(sh), 1e-6, xd, 4)
+    assert_bf16(o.layer_norm_modulate_bf16(xb, s, sh, 4, 1e-6), host_bits(xd), what="AdaLN in place")

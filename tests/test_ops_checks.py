@@ -1,0 +1,81 @@
+"""HipOps' shape and dtype rules on the host: the reference's checks
+(ops/Ops.scala:36-93, ops/AttentionOps.scala:129-223, ops/LinearOps.scala:92-106,
+ops/MemoryOps.scala:68-84) refuse the same calls with the same messages,
+before anything is launched. CPU tensors only: a call that passed the shape
+rules would stop at "tensors live in device memory"."""
+
+import pytest
+import torch
+
+from drift_amd import ops as d
+
+
+@pytest.fixture(scope="module")
+def hip():
+    return d.HipOps()
+
+
+def f32(*shape):
+    return torch.zeros(shape, dtype=torch.float32)
+
+
+def bf16(*shape):
+    return torch.zeros(shape, dtype=torch.bfloat16)
+
+
+def test_mismatched_shapes_are_refused(hip):
+    # CpuOpsTests.scala:58-70
+    with pytest.raises(ValueError, match="equal shapes"):
+        hip.gated(d.Activation.Silu, f32(2), f32(3), f32(2))
+
+
+def test_row_vectors_must_match_rows(hip):
+    with pytest.raises(ValueError, match=r"rmsNorm: \[3\] for rows of 4"):
+        hip.rmsNorm(f32(2, 4), f32(3), 1e-6, 0.0, f32(2, 4))
+    with pytest.raises(ValueError, match="takes F32, not BF16"):
+        hip.rmsNorm(f32(2, 4), bf16(4), 1e-6, 0.0, f32(2, 4))
+    with pytest.raises(ValueError, match="one type"):
+        hip.rmsNorm(bf16(2, 4), f32(4), 1e-6, 0.0, f32(2, 4))
+    with pytest.raises(ValueError, match=r"modulate: \[5\] for rows of 4"):
+        hip.modulate(f32(2, 4), f32(4), f32(5), f32(2, 4))
+
+
+def test_rope_rules(hip):
+    rope = d.Rope(1e4, 128, d.RopeLayout.Neox)
+    with pytest.raises(ValueError, match="rope takes"):
+        hip.rope(f32(4, 128), torch.zeros(4, dtype=torch.int32), rope, f32(4, 128))
+    with pytest.raises(ValueError, match="positions are I32, not F32"):
+        hip.rope(f32(4, 2, 128), f32(4), rope, f32(4, 2, 128))
+    with pytest.raises(ValueError, match=r"positions \[4\], expected \[3, 4\]"):
+        mrope = d.Rope(1e6, 64, d.RopeLayout.Neox, d.RopeSections.Contiguous(11, 11, 10))
+        hip.rope(f32(4, 2, 128), torch.zeros(4, dtype=torch.int32), mrope, f32(4, 2, 128))
+    with pytest.raises(ValueError, match="axes of"):
+        axes = d.Rope(1e3, 128, d.RopeLayout.Interleaved, d.RopeSections.Axes([16, 24, 23]))
+        hip.rope(f32(4, 2, 128), torch.zeros(3, 4, dtype=torch.int32), axes, f32(4, 2, 128))
+    with pytest.raises(ValueError, match="130 rotary dimensions in heads of 128"):
+        hip.rope(f32(4, 2, 128), torch.zeros(4, dtype=torch.int32), d.Rope(1e4, 130), f32(4, 2, 128))
+
+
+def test_rope_table_rules(hip):
+    with pytest.raises(ValueError, match="ropeTable: tables"):
+        hip.ropeTable(f32(4, 2, 128), f32(4, 65), f32(4, 65), f32(4, 2, 128))
+    with pytest.raises(ValueError, match="ropeTable: tables"):
+        hip.ropeTable(f32(4, 2, 128), f32(3, 64), f32(3, 64), f32(4, 2, 128))
+
+
+def test_embedding_rules(hip):
+    table = d.Q8_0Table(torch.zeros(10, 68, dtype=torch.uint8), 64)
+    with pytest.raises(ValueError, match="ids are I32"):
+        hip.embedding(table, torch.zeros(3, dtype=torch.int64), f32(3, 64))
+    with pytest.raises(ValueError, match=r"out \[3, 32\] for 3 rows of 64"):
+        hip.embedding(table, torch.zeros(3, dtype=torch.int32), f32(3, 32))
+
+
+def test_convert_rules(hip):
+    with pytest.raises(ValueError, match="no conversion from BF16 to F16"):
+        hip.convert(bf16(4), torch.zeros(4, dtype=torch.float16))
+
+
+def test_host_tensors_are_refused_before_launch(hip):
+    with pytest.raises(ValueError, match="device memory"):
+        hip.rmsNorm(f32(2, 4), f32(4), 1e-6, 0.0, f32(2, 4))
