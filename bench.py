@@ -52,8 +52,10 @@ class Kernel:
         self.times_ms = []
 
 
-def sets_for(bytes_per_call: int, floor: int = 2) -> int:
-    return max(floor, math.ceil(MALL_BYTES / max(bytes_per_call, 1)) + 1)
+def sets_for(bytes_per_call: int, floor: int = 2, cap: int = 64) -> int:
+    """Buffer sets to rotate through so the sets total more than 512 MB (the
+    decode shapes are capped: a decode step's activations do sit in cache)."""
+    return min(cap, max(floor, math.ceil(MALL_BYTES / max(bytes_per_call, 1)) + 1))
 
 
 def gen(seed):
@@ -72,7 +74,7 @@ def make_kernels(hip: d.HipOps):
     # C2 decode: RMSNorm bf16 [B, 4096] (w f32, eps 1e-5) and SwiGLU [B, 14336]
     for b in (1, 8, 64):
         nbytes = 2 * b * 4096 * 2 + 4096 * 4
-        n = sets_for(nbytes, 8)
+        n = sets_for(nbytes, 8, 8)
         xs = [randn_bf16((b, 4096), 10 + i) for i in range(n)]
         outs = [torch.empty_like(xs[0]) for _ in range(n)]
         w = (1 + 0.1 * torch.randn(4096, generator=gen(1), device=DEV)).float()
@@ -80,7 +82,7 @@ def make_kernels(hip: d.HipOps):
                               lambda i, xs=xs, outs=outs, w=w: hip.rmsNorm(xs[i % len(xs)], w, 1e-5, 0.0,
                                                                            outs[i % len(outs)])))
         nbytes = 3 * b * 14336 * 2
-        n = sets_for(nbytes, 8)
+        n = sets_for(nbytes, 8, 8)
         gs = [randn_bf16((b, 14336), 100 + i) for i in range(n)]
         us = [randn_bf16((b, 14336), 200 + i) for i in range(n)]
         os_ = [torch.empty_like(gs[0]) for _ in range(n)]
@@ -190,9 +192,11 @@ def cpu_baseline(kernels, budget_s: float):
         x = bits((units, 3072))
         return lambda: o.activation_bf16(1, x)
 
+    cos, sin = o.wan_angles(21, 30, 52)  # Wan keeps a grid's tables (models/Wan.scala:324-330)
+
     def rope3d(units):
-        x = bits((units, 24, 128))
-        return lambda: o.rope_3d_bf16(x, 21, 30, 52)
+        x = o.from_bf16(bits((units, 24, 128)))
+        return lambda: o.to_bf16(o.rope_table(x, cos[:units], sin[:units]))
 
     work = {}
     for b in (1, 8, 64):

@@ -22,13 +22,18 @@ __device__ __forceinline__ float bf16_hi(uint32_t pair) { return __uint_as_float
 
 // Float to BF16 bits as CpuOps.toBfloat16 rounds (ops/CpuOps.scala:426-431):
 // nearest even on the bit pattern; a NaN keeps its top half, quiet bit set.
-__device__ __forceinline__ uint32_t bf16_bits(float v) {
-  const uint32_t b = __float_as_uint(v);
-  const uint32_t rounded = (b + 0x7fffu + ((b >> 16) & 1u)) >> 16;
-  return (v != v) ? ((b >> 16) | 0x40u) : rounded;
+// gfx950's v_cvt_pk_bf16_f32 does exactly this, two values per instruction
+// (checked on the device over every class of pattern, NaN payloads and ties
+// included: tests/test_gpu_elementwise.py::test_convert_round_trips).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
+  const f32x2_t v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
 
-__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) { return bf16_bits(lo) | (bf16_bits(hi) << 16); }
+__device__ __forceinline__ uint32_t bf16_bits(float v) { return pack_bf16(v, 0.0f) & 0xffffu; }
 
 // ---------------------------------------------------------------- element types
 
@@ -36,9 +41,20 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) { return bf16_
 template <typename T>
 struct Chunk;
 
+// Raw: the chunk as loaded (16 bytes in four VGPRs); unpack: its values as
+// float. opaque() hides a raw chunk's value from the compiler, so a second
+// pass re-unpacks it instead of keeping every converted value alive.
 template <>
 struct Chunk<float> {
   static constexpr int N = 4;
+  using Raw = uint4;
+  __device__ __forceinline__ static Raw load_raw(const float* p) { return *reinterpret_cast<const uint4*>(p); }
+  __device__ __forceinline__ static void unpack(const Raw& q, float (&v)[4]) {
+    v[0] = __uint_as_float(q.x);
+    v[1] = __uint_as_float(q.y);
+    v[2] = __uint_as_float(q.z);
+    v[3] = __uint_as_float(q.w);
+  }
   __device__ __forceinline__ static void load(const float* p, float (&v)[4]) {
     const float4 q = *reinterpret_cast<const float4*>(p);
     v[0] = q.x;
@@ -54,6 +70,18 @@ struct Chunk<float> {
 template <>
 struct Chunk<uint16_t> {
   static constexpr int N = 8;
+  using Raw = uint4;
+  __device__ __forceinline__ static Raw load_raw(const uint16_t* p) { return *reinterpret_cast<const uint4*>(p); }
+  __device__ __forceinline__ static void unpack(const Raw& q, float (&v)[8]) {
+    v[0] = bf16_lo(q.x);
+    v[1] = bf16_hi(q.x);
+    v[2] = bf16_lo(q.y);
+    v[3] = bf16_hi(q.y);
+    v[4] = bf16_lo(q.z);
+    v[5] = bf16_hi(q.z);
+    v[6] = bf16_lo(q.w);
+    v[7] = bf16_hi(q.w);
+  }
   __device__ __forceinline__ static void load(const uint16_t* p, float (&v)[8]) {
     const uint4 q = *reinterpret_cast<const uint4*>(p);
     v[0] = bf16_lo(q.x);
@@ -70,6 +98,8 @@ struct Chunk<uint16_t> {
         make_uint4(pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]), pack_bf16(v[4], v[5]), pack_bf16(v[6], v[7]));
   }
 };
+
+__device__ __forceinline__ void opaque(uint4& q) { asm volatile("" : "+v"(q.x), "+v"(q.y), "+v"(q.z), "+v"(q.w)); }
 
 // Scalar element access for the awkward-shape paths.
 __device__ __forceinline__ float load_one(const float* p) { return *p; }

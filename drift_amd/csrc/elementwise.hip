@@ -13,28 +13,24 @@
 // and, where the reference's own double result is quantized (1 + tanh u and
 // 1 + erf x below 2^-29 hold a whole number of 2^-53 steps, the spacing of
 // doubles just above -1), the same quantization is applied, so the results
-// agree with the reference there too. BF16 outputs use the hardware exp and
-// reciprocal (about 1e-6 relative, far below a bf16 ulp); F32 outputs use the
-// accurate library functions.
+// agree with the reference there too. F32 outputs use the accurate library
+// exp and IEEE division. BF16 outputs use the hardware exp2 and reciprocal
+// (v_exp_f32, v_rcp_f32: about 1e-6 relative, far below a bf16 ulp, and BF16
+// output is all the precision they feed), with GELU-tanh's sigmoid form
+// folded to one exp2 argument:
+//   gelu_tanh(v) = v h,  h = 1/(1 + 2^(v (c0 + c1 v^2))),
+//   c0 = -2 log2(e) sqrt(2/pi), c1 = c0 * 0.044715.
 #include "common.hpp"
 
 namespace drift {
 namespace {
 
 template <bool ACCURATE>
-__device__ __forceinline__ float exp_of(float x) {
-  if constexpr (ACCURATE)
-    return expf(x);
-  else
-    return __expf(x);
-}
-
-template <bool ACCURATE>
 __device__ __forceinline__ float divide(float a, float b) {
   if constexpr (ACCURATE)
     return a / b;
   else
-    return __fdividef(a, b);
+    return a * __builtin_amdgcn_rcpf(b);
 }
 
 // A double's 1 + t for t in (-1, -1/2]: a whole number of 2^-53 steps. t here
@@ -46,22 +42,53 @@ __device__ __forceinline__ float quantize_2m53(float t) {
 
 template <bool ACCURATE>
 __device__ __forceinline__ float sigmoid_of(float v) {
-  const float e = exp_of<ACCURATE>(-fabsf(v));
-  const float r = divide<ACCURATE>(1.0f, 1.0f + e);
-  return v >= 0.0f ? r : e * r;
+  if constexpr (ACCURATE) {
+    const float e = expf(-fabsf(v));
+    const float r = 1.0f / (1.0f + e);
+    return v >= 0.0f ? r : e * r;
+  } else {
+    const float e = __builtin_amdgcn_exp2f(-1.44269504088896341f * fabsf(v));
+    const float r = __builtin_amdgcn_rcpf(1.0f + e);
+    return v >= 0.0f ? r : e * r;
+  }
+}
+
+// GELU-tanh of M values for BF16 outputs, in place (see the file comment).
+// The tail quantization runs only when some lane has a value that needs it.
+template <int M>
+__device__ __forceinline__ void gelu_tanh_fast(float (&v)[M]) {
+  constexpr float c0 = -2.30220819814432500f;  // -2 log2(e) sqrt(2/pi)
+  constexpr float c1 = -0.10294323958002350f;  // c0 * 0.044715
+  float h[M];
+  bool tail = false;
+#pragma unroll
+  for (int j = 0; j < M; ++j) {
+    const float a = v[j] * fmaf(c1, v[j] * v[j], c0);
+    h[j] = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(a));  // (1 + tanh u) / 2
+    tail |= h[j] < 0x1p-30f;
+  }
+  if (__builtin_expect(__any(tail), 0)) {
+#pragma unroll
+    for (int j = 0; j < M; ++j) h[j] = h[j] < 0x1p-30f ? rintf(h[j] * 0x1p54f) * 0x1p-54f : h[j];
+  }
+#pragma unroll
+  for (int j = 0; j < M; ++j) v[j] *= h[j];
 }
 
 template <bool ACCURATE>
 __device__ __forceinline__ float activate(int kind, float v) {
   switch (kind) {
-    case DRIFT_SILU: {
-      const float e = exp_of<ACCURATE>(-fabsf(v));
-      return divide<ACCURATE>(v >= 0.0f ? v : v * e, 1.0f + e);
-    }
+    case DRIFT_SILU:
+      return v * sigmoid_of<ACCURATE>(v);
     case DRIFT_GELU_TANH: {
+      if constexpr (!ACCURATE) {
+        float one[1] = {v};
+        gelu_tanh_fast(one);
+        return one[0];
+      }
       const float u = 0.7978845608028654f * (v + 0.044715f * v * v * v);
-      const float e = exp_of<ACCURATE>(-2.0f * fabsf(u));
-      const float t = divide<ACCURATE>(u >= 0.0f ? 2.0f : 2.0f * e, 1.0f + e);  // 1 + tanh(u)
+      const float e = expf(-2.0f * fabsf(u));
+      const float t = (u >= 0.0f ? 2.0f : 2.0f * e) / (1.0f + e);  // 1 + tanh(u)
       return 0.5f * v * quantize_2m53(t);
     }
     case DRIFT_GELU_ERF: {
@@ -98,10 +125,20 @@ __global__ void __launch_bounds__(256) activation_kernel(const T* x, T* out, int
     float a[N], b[N];
     Chunk<T>::load(x + i * N, a);
     Chunk<T>::load(x + (i + stride) * N, b);
+    if constexpr (KIND == DRIFT_GELU_TANH && !A) {
 #pragma unroll
-    for (int j = 0; j < N; ++j) {
-      a[j] = activate<A>(k, scale * a[j]);
-      b[j] = activate<A>(k, scale * b[j]);
+      for (int j = 0; j < N; ++j) {
+        a[j] *= scale;
+        b[j] *= scale;
+      }
+      gelu_tanh_fast(a);
+      gelu_tanh_fast(b);
+    } else {
+#pragma unroll
+      for (int j = 0; j < N; ++j) {
+        a[j] = activate<A>(k, scale * a[j]);
+        b[j] = activate<A>(k, scale * b[j]);
+      }
     }
     Chunk<T>::store(out + i * N, a);
     Chunk<T>::store(out + (i + stride) * N, b);
@@ -109,8 +146,14 @@ __global__ void __launch_bounds__(256) activation_kernel(const T* x, T* out, int
   if (i < chunks) {
     float a[N];
     Chunk<T>::load(x + i * N, a);
+    if constexpr (KIND == DRIFT_GELU_TANH && !A) {
 #pragma unroll
-    for (int j = 0; j < N; ++j) a[j] = activate<A>(k, scale * a[j]);
+      for (int j = 0; j < N; ++j) a[j] *= scale;
+      gelu_tanh_fast(a);
+    } else {
+#pragma unroll
+      for (int j = 0; j < N; ++j) a[j] = activate<A>(k, scale * a[j]);
+    }
     Chunk<T>::store(out + i * N, a);
   }
   const int64_t tail = chunks * N + tid;

@@ -15,6 +15,8 @@
 // another order.
 #include "common.hpp"
 
+#include <algorithm>
+
 namespace drift {
 namespace {
 
@@ -240,6 +242,95 @@ __global__ void __launch_bounds__(256) layer_norm_rows_scalar(const T* x, const 
   }
 }
 
+// AdaLN over one sample's rows, one wave per row: the sample's (1 + scale,
+// shift) are made once per block, in double, into LDS laid out
+// [value of chunk][chunk], so the 64 lanes of a wave reading value j of their
+// chunks read 64 consecutive 16-byte entries (no bank conflicts). Blocks are
+// persistent over their sample's rows (grid.y = sample), so the table costs
+// one pass per block, not per row.
+//
+// The mean and variance come from one pass over the row in double about its
+// first value x0 (sums of d = x - x0 and d^2): the same as the reference's two
+// passes to the last bits, since |mean - x0| is a few standard deviations at
+// most. n = float((x - mean) * factor) is the reference layerNorm's F32
+// result; out = n * (1 + scale) + shift in double, rounded once, as modulate.
+template <typename T, int K, bool FULL>
+__global__ void __launch_bounds__(512) adaln_rows(const T* x, const float* scale, const float* shift, T* out,
+                                                  int64_t rows, int cols, int64_t rows_per_sample, float eps) {
+  constexpr int N = Chunk<T>::N;
+  using Raw = typename Chunk<T>::Raw;
+  extern __shared__ double2 table[];  // [N][chunks]
+  // with whole rows of K wave-chunks the table's stride is a constant, so
+  // every LDS read takes its offset as an immediate
+  const int chunks = FULL ? K * kWave : cols / N;
+  const int64_t sample = blockIdx.y;
+  const float* sc = scale + sample * cols;
+  const float* sh = shift + sample * cols;
+  for (int c = threadIdx.x; c < cols; c += blockDim.x)
+    table[(c % N) * chunks + c / N] = make_double2(1.0 + (double)sc[c], (double)sh[c]);
+  __syncthreads();
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
+  const int64_t first = sample * rows_per_sample;
+  const int64_t end = min(rows, first + rows_per_sample);
+  const int64_t stride = (int64_t)gridDim.x * waves;
+  int64_t row = first + (int64_t)blockIdx.x * waves + wave;
+  Raw raw[K];
+  auto load_row = [&](int64_t r, Raw(&into)[K]) {
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const int c = k * kWave + lane;
+      if (FULL || c < chunks) into[k] = Chunk<T>::load_raw(x + r * cols + c * N);
+    }
+  };
+  if (row < end) load_row(row, raw);
+  for (; row < end; row += stride) {
+    Raw next[K];
+    if (row + stride < end) load_row(row + stride, next);  // in flight while this row computes
+    float first_value[N];
+    Chunk<T>::unpack(raw[0], first_value);
+    const double x0 = (double)__shfl(first_value[0], 0);
+    double s1 = 0.0, s2 = 0.0;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      if (FULL || k * kWave + lane < chunks) {
+        float v[N];
+        Chunk<T>::unpack(raw[k], v);
+#pragma unroll
+        for (int j = 0; j < N; ++j) {
+          const double d = (double)v[j] - x0;
+          s1 += d;
+          s2 = fma(d, d, s2);
+        }
+      }
+    }
+    s1 = group_sum<64>(s1);
+    s2 = group_sum<64>(s2);
+    const double m1 = s1 / (double)cols;  // mean - x0
+    const double mean = x0 + m1;
+    const double variance = fmax(s2 / (double)cols - m1 * m1, 0.0);
+    const double factor = 1.0 / sqrt(variance + (double)eps);
+    const double offset = -mean * factor;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const int c = k * kWave + lane;
+      if (FULL || c < chunks) {
+        opaque(raw[k]);
+        float v[N], o[N];
+        Chunk<T>::unpack(raw[k], v);
+#pragma unroll
+        for (int j = 0; j < N; ++j) {
+          const float n = (float)fma((double)v[j], factor, offset);
+          const double2 t = table[j * chunks + c];
+          o[j] = (float)fma((double)n, t.x, t.y);
+        }
+        Chunk<T>::store(out + row * cols + c * N, o);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < K; ++k) raw[k] = next[k];
+  }
+}
+
 // ------------------------------------------------------------------ modulate
 
 template <typename T>
@@ -338,6 +429,44 @@ int rms_norm(const char* entry, T* x, const T* y, const float* weight, T* out, i
   return launched(entry);
 }
 
+// AdaLN through adaln_rows: whole-chunk rows of at most 64 chunks per lane
+// ... 16 chunks per lane, a table that fits LDS, and enough rows per sample to
+// pay for it. Returns -1 when the shape does not qualify.
+template <typename T>
+int adaln_launch(const T* x, const float* scale, const float* shift, T* out, int64_t rows, int cols,
+                 int64_t rows_per_sample, float eps, hipStream_t s) {
+  constexpr int N = Chunk<T>::N;
+  const int64_t samples = ceil_div(rows, rows_per_sample);
+  const size_t lds = (size_t)cols * sizeof(double2);
+  if (cols % N != 0 || lds > 64 * 1024 || rows_per_sample < 64 || samples > 65535) return -1;
+  const int chunks = cols / N;
+  const int per_lane = (int)ceil_div(chunks, kWave);
+  // about three 8-wave blocks per CU over the whole launch
+  const int64_t per_sample = std::max<int64_t>(1, std::min<int64_t>(ceil_div(rows_per_sample, 8),
+                                                                    ceil_div(3 * 256, samples)));
+  const dim3 grid((unsigned)per_sample, (unsigned)samples);
+#define DRIFT_ADALN_CASE(K)                                                                                     \
+  if (per_lane <= K) {                                                                                          \
+    if (chunks == K * kWave)                                                                                    \
+      hipLaunchKernelGGL((adaln_rows<T, K, true>), grid, dim3(512), lds, s, x, scale, shift, out, rows, cols,  \
+                         rows_per_sample, eps);                                                                 \
+    else                                                                                                        \
+      hipLaunchKernelGGL((adaln_rows<T, K, false>), grid, dim3(512), lds, s, x, scale, shift, out, rows, cols, \
+                         rows_per_sample, eps);                                                                 \
+    return 0;                                                                                                   \
+  }
+  DRIFT_ADALN_CASE(1)
+  DRIFT_ADALN_CASE(2)
+  DRIFT_ADALN_CASE(3)
+  DRIFT_ADALN_CASE(4)
+  DRIFT_ADALN_CASE(6)
+  DRIFT_ADALN_CASE(8)
+  DRIFT_ADALN_CASE(12)
+  DRIFT_ADALN_CASE(16)
+#undef DRIFT_ADALN_CASE
+  return -1;
+}
+
 template <typename T, bool MODULATE>
 int layer_norm(const char* entry, const T* x, const float* weight, const float* bias, T* out, int64_t rows,
                int32_t cols, int64_t rows_per_sample, float eps, void* stream) {
@@ -351,6 +480,8 @@ int layer_norm(const char* entry, const T* x, const float* weight, const float* 
   const hipStream_t s = (hipStream_t)stream;
   const bool vector_ok =
       aligned16(x) && aligned16(out) && (!weight || aligned16(weight)) && (!bias || aligned16(bias));
+  if (MODULATE && vector_ok && adaln_launch<T>(x, weight, bias, out, rows, cols, rows_per_sample, eps, s) == 0)
+    return launched(entry);
   const RowPlan plan = plan_rows<T>(rows, cols, vector_ok);
   if (plan.per_lane == 0) {
     hipLaunchKernelGGL((layer_norm_rows_scalar<T, MODULATE>), dim3(grid_for(rows, 1)), dim3(256), 0, s, x, weight,

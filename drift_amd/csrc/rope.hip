@@ -18,6 +18,9 @@
 // rounded to float; rope_3d makes exactly those values.
 #include "common.hpp"
 
+#include <algorithm>
+#include <climits>
+
 namespace drift {
 namespace {
 
@@ -60,6 +63,14 @@ __device__ __forceinline__ void token_angles(const RopeArgs& p, const int32_t* p
 __device__ __forceinline__ void turn(double a, double b, double c, double s, float& first, float& second) {
   first = (float)(a * c - b * s);
   second = (float)(a * s + b * c);
+}
+
+// The same turn with one rounding per output: a*c - b*s as fma(a, c, -(b*s)).
+// It differs from the two-rounding form only when the double result lies
+// within a double ulp of a float rounding boundary (about 2^-28 of values).
+__device__ __forceinline__ void turn_fused(double a, double b, double c, double s, float& first, float& second) {
+  first = (float)fma(a, c, -(b * s));
+  second = (float)fma(a, s, b * c);
 }
 
 // Pair slot j of one head (slots cover the head: j < rotary/2 turn a pair,
@@ -232,6 +243,112 @@ __global__ void __launch_bounds__(256) rope_3d_kernel(const T* x, T* out, Rope3d
   }
 }
 
+// Wan's angles depend on one axis position each, so a block makes them once
+// per (axis, position, pair of that axis) into LDS, (float cos, float sin) of
+// the double angle exactly as the host tables hold them: frames * p0 +
+// rows * p1 + cols * p2 entries (2184 for a 21 x 30 x 52 grid of 64 pairs)
+// instead of 64 sincos per token. A wave then takes a token at a time (its
+// next token's chunks already loading), looks up its pairs and turns them.
+// With a, b bf16 or F32 and c, s floats, a*c and b*s are exact in double, so
+// fma(a, c, -b*s) is the reference's a*c - b*s rounded once.
+struct AxisTables {
+  int32_t base1, base2;  // first row and column entries; frame entries start at 0
+  int32_t entries;
+  int64_t stride_mod;  // (blocks * waves) mod grid: a wave's step through the grid
+};
+
+template <typename T, bool FIXED>
+__global__ void __launch_bounds__(512) rope_3d_axes(const T* x, T* out, Rope3dArgs p, AxisTables at) {
+  constexpr int N = Chunk<T>::N;
+  using Raw = typename Chunk<T>::Raw;
+  extern __shared__ float2 axis_cs[];
+  const int p0 = p.pairs0, p1 = p.pairs1, p2 = p.dim / 2 - p0 - p1;
+  for (int e = threadIdx.x; e < at.entries; e += blockDim.x) {
+    int position, pair;
+    if (e < at.base1) {
+      position = e / p0;
+      pair = e % p0;
+    } else if (e < at.base2) {
+      position = (e - at.base1) / p1;
+      pair = p0 + (e - at.base1) % p1;
+    } else {
+      position = (e - at.base2) / p2;
+      pair = p0 + p1 + (e - at.base2) % p2;
+    }
+    double sn, cn;
+    sincos((double)position / p.denominator[pair], &sn, &cn);
+    axis_cs[e] = make_float2((float)cn, (float)sn);
+  }
+  __syncthreads();
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int waves = blockDim.x >> 6;
+  const int per_token = p.heads * p.dim / N;  // chunks of a token
+  const int per_head = p.dim / N;
+  const int64_t stride = (int64_t)gridDim.x * waves;
+  int64_t t = (int64_t)blockIdx.x * waves + wave;
+  int64_t g = (p.token_offset + t) % p.grid;
+  const int plane = p.rows * p.cols;
+  constexpr int kMaxChunks = 8;  // per lane per token, in flight at once
+  const int rounds = (per_token + kMaxChunks * kWave - 1) / (kMaxChunks * kWave);
+  for (; t < p.tokens; t += stride) {
+    const int frame = (int)(g / plane), rem = (int)(g % plane);
+    const int base[3] = {frame * p0, at.base1 + (rem / p.cols) * p1, at.base2 + (rem % p.cols) * p2};
+    const T* xt = x + t * p.heads * p.dim;
+    T* ot = out + t * p.heads * p.dim;
+    // the lane's pairs' cos and sin, when they are the same in every chunk
+    double fc[N / 2], fs[N / 2];
+    if constexpr (FIXED) {
+      const int d0 = (lane % per_head) * N;
+#pragma unroll
+      for (int i = 0; i < N / 2; ++i) {
+        const int m = d0 / 2 + i;
+        const int e = m < p0 ? base[0] + m : (m < p0 + p1 ? base[1] + m - p0 : base[2] + m - p0 - p1);
+        const float2 q = axis_cs[e];
+        fc[i] = q.x;
+        fs[i] = q.y;
+      }
+    }
+    for (int r = 0; r < rounds; ++r) {
+      Raw raw[kMaxChunks];
+#pragma unroll
+      for (int k = 0; k < kMaxChunks; ++k) {
+        const int q = (r * kMaxChunks + k) * kWave + lane;
+        if (q < per_token) raw[k] = Chunk<T>::load_raw(xt + q * N);
+      }
+#pragma unroll
+      for (int k = 0; k < kMaxChunks; ++k) {
+        const int q = (r * kMaxChunks + k) * kWave + lane;
+        if (q < per_token) {
+          float v[N];
+          Chunk<T>::unpack(raw[k], v);
+          const int d0 = (q % per_head) * N;
+#pragma unroll
+          for (int i = 0; i < N / 2; ++i) {
+            double c, sn;
+            if constexpr (FIXED) {
+              c = fc[i];
+              sn = fs[i];
+            } else {
+              const int m = d0 / 2 + i;
+              const int e = m < p0 ? base[0] + m : (m < p0 + p1 ? base[1] + m - p0 : base[2] + m - p0 - p1);
+              const float2 cs = axis_cs[e];
+              c = cs.x;
+              sn = cs.y;
+            }
+            const double a = v[2 * i], b = v[2 * i + 1];
+            v[2 * i] = (float)fma(a, c, -(b * sn));
+            v[2 * i + 1] = (float)fma(a, sn, b * c);
+          }
+          Chunk<T>::store(ot + q * N, v);
+        }
+      }
+    }
+    g += at.stride_mod;
+    if (g >= p.grid) g -= p.grid;
+  }
+}
+
 // ------------------------------------------------------------------ per-head RMSNorm + rope
 
 struct QkArgs {
@@ -359,6 +476,107 @@ __global__ void __launch_bounds__(256) qk_norm_rope_chunks(const T* q, const T* 
   }
 }
 
+// The fast path for whole-chunk heads with every value turning, one wave per
+// token: the token's pairs' cos and sin (one sincos per lane) into the wave's
+// LDS slice, the norm weights (+ offset, in double) into LDS once per block;
+// then passes of 64 / G heads, G lanes per head each holding two chunks (NeoX:
+// a chunk and its partner; otherwise chunks i and i + G), every pass's loads
+// issued before the first pass computes.
+template <typename T, int G>
+__global__ void __launch_bounds__(256) qk_norm_rope_waves(const T* q, const T* k, T* q_out, T* k_out,
+                                                          const float* q_weight, const float* k_weight,
+                                                          const int32_t* positions, QkArgs a) {
+  constexpr int N = Chunk<T>::N;
+  using Raw = typename Chunk<T>::Raw;
+  constexpr int kHeadsPerPass = kWave / G;
+  constexpr int kMaxPasses = 4;
+  __shared__ double2 cs_all[4][kMaxPairs / 2];  // dim = 2 N G <= 2 N 64, pairs = N G
+  __shared__ double weights[2][2 * kMaxPairs];
+  const RopeArgs& p = a.rope;
+  const int dim = 2 * N * G, half = N * G;
+  for (int d = threadIdx.x; d < dim; d += blockDim.x) {
+    weights[0][d] = (double)q_weight[d] + (double)a.offset;
+    weights[1][d] = (double)k_weight[d] + (double)a.offset;
+  }
+  __syncthreads();
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  double2* cs = cs_all[wave];
+  const int rows = a.q_heads + a.kv_heads;
+  const int passes = (rows + kHeadsPerPass - 1) / kHeadsPerPass;
+  const int i0 = lane % G;
+  const int d0 = i0 * N, d1 = half + i0 * N;
+  for (int64_t t = (int64_t)blockIdx.x * 4 + wave; t < p.tokens; t += (int64_t)gridDim.x * 4) {
+    for (int j = lane; j < half; j += kWave) {
+      const int32_t position = positions[(int64_t)rope_section(j, p) * p.tokens + t];
+      double sn, cn;
+      sincos((double)((float)position * p.inverse[j]), &sn, &cn);
+      cs[j] = make_double2(cn, sn);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    for (int first = 0; first < passes; first += kMaxPasses) {
+      Raw r0[kMaxPasses], r1[kMaxPasses];
+#pragma unroll
+      for (int s = 0; s < kMaxPasses; ++s) {
+        const int h = (first + s) * kHeadsPerPass + lane / G;
+        if (first + s < passes && h < rows) {
+          const T* xh = h < a.q_heads ? q + (t * a.q_heads + h) * dim : k + (t * a.kv_heads + (h - a.q_heads)) * dim;
+          r0[s] = Chunk<T>::load_raw(xh + d0);
+          r1[s] = Chunk<T>::load_raw(xh + d1);
+        }
+      }
+#pragma unroll
+      for (int s = 0; s < kMaxPasses; ++s) {
+        if (first + s >= passes) break;
+        const int h = (first + s) * kHeadsPerPass + lane / G;
+        const bool live = h < rows;
+        const bool query = h < a.q_heads;
+        float v0[N], v1[N];
+        Chunk<T>::unpack(r0[s], v0);
+        Chunk<T>::unpack(r1[s], v1);
+        double squares = 0.0;
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+          squares = fma((double)v0[i], (double)v0[i], squares);
+          squares = fma((double)v1[i], (double)v1[i], squares);
+        }
+        squares = group_sum<G>(squares);
+        if (live) {
+          const double factor = 1.0 / sqrt(squares / (double)dim + (double)a.eps);
+          const double* w = weights[query ? 0 : 1];
+#pragma unroll
+          for (int i = 0; i < N; ++i) {
+            v0[i] = (float)((double)v0[i] * factor * w[d0 + i]);
+            v1[i] = (float)((double)v1[i] * factor * w[d1 + i]);
+          }
+          if (p.layout == DRIFT_ROPE_NEOX) {
+#pragma unroll
+            for (int i = 0; i < N; ++i) {
+              const double2 c = cs[d0 + i];
+              turn_fused(v0[i], v1[i], c.x, c.y, v0[i], v1[i]);
+            }
+          } else {
+#pragma unroll
+            for (int i = 0; i < N; i += 2) {
+              const double2 c0 = cs[(d0 + i) / 2], c1 = cs[(d1 + i) / 2];
+              turn_fused(v0[i], v0[i + 1], c0.x, c0.y, v0[i], v0[i + 1]);
+              turn_fused(v1[i], v1[i + 1], c1.x, c1.y, v1[i], v1[i + 1]);
+            }
+          }
+          T* oh = query ? q_out + (t * a.q_heads + h) * dim : k_out + (t * a.kv_heads + (h - a.q_heads)) * dim;
+          Chunk<T>::store(oh + d0, v0);
+          Chunk<T>::store(oh + d1, v1);
+        }
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();  // cs is remade for the next token
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+}
+
 // ------------------------------------------------------------------ launch layer
 
 int check_rope(const char* entry, int32_t tokens, int32_t heads, int32_t dim, int32_t rotary, int32_t layout,
@@ -456,7 +674,8 @@ int rope_3d(const char* entry, const T* x, T* out, int64_t tokens, int32_t heads
   clear_error();
   if (tokens < 0 || heads < 0) return refuse("%s: %lld tokens of %d heads", entry, (long long)tokens, heads);
   if (dim <= 0 || dim % 2 != 0 || dim > 2 * kMaxPairs) return refuse("%s: heads of %d values", entry, dim);
-  if (frames <= 0 || rows <= 0 || cols <= 0) return refuse("%s: a %d x %d x %d grid", entry, frames, rows, cols);
+  if (frames <= 0 || rows <= 0 || cols <= 0 || (int64_t)frames * rows * cols > INT32_MAX)
+    return refuse("%s: a %d x %d x %d grid", entry, frames, rows, cols);
   if (token_offset < 0) return refuse("%s: token offset %lld", entry, (long long)token_offset);
   if (tokens * heads == 0) return 0;
   if (!x || !out) return refuse("%s: null x or out", entry);
@@ -485,8 +704,24 @@ int rope_3d(const char* entry, const T* x, T* out, int64_t tokens, int32_t heads
   }
   constexpr int N = Chunk<T>::N;
   const bool chunked = aligned16(x) && aligned16(out) && dim % N == 0;
-  const dim3 grid(grid_for(tokens, 1, 1 << 16));
   const hipStream_t st = (hipStream_t)stream;
+  const int64_t entries = (int64_t)frames * axes[0] + (int64_t)rows * axes[1] + (int64_t)cols * axes[2];
+  if (chunked && entries * (int64_t)sizeof(float2) <= 64 * 1024) {
+    AxisTables at;
+    at.base1 = frames * axes[0];
+    at.base2 = at.base1 + rows * axes[1];
+    at.entries = (int32_t)entries;
+    const int waves = 8;
+    const unsigned blocks = (unsigned)std::min<int64_t>(ceil_div(tokens, waves), 512);
+    at.stride_mod = ((int64_t)blocks * waves) % p.grid;
+    const size_t lds = (size_t)entries * sizeof(float2);
+    if ((64 % (dim / N)) == 0)
+      hipLaunchKernelGGL((rope_3d_axes<T, true>), dim3(blocks), dim3(64 * waves), lds, st, x, out, p, at);
+    else
+      hipLaunchKernelGGL((rope_3d_axes<T, false>), dim3(blocks), dim3(64 * waves), lds, st, x, out, p, at);
+    return launched(entry);
+  }
+  const dim3 grid(grid_for(tokens, 1, 1 << 16));
   if (chunked)
     hipLaunchKernelGGL((rope_3d_kernel<T, true>), grid, dim3(256), 0, st, x, out, p);
   else
@@ -520,11 +755,12 @@ int qk_norm_rope(const char* entry, const T* q, const T* k, T* q_out, T* k_out, 
   const dim3 grid(grid_for(tokens, 1, 1 << 16));
   const hipStream_t st = (hipStream_t)stream;
   if (whole) {
+    const dim3 waves_grid(grid_for(tokens, 4, 1 << 16));
     switch (lanes_per_head) {
-#define DRIFT_QK_CASE(G)                                                                                             \
-  case G:                                                                                                            \
-    hipLaunchKernelGGL((qk_norm_rope_chunks<T, G>), grid, dim3(256), 0, st, q, k, q_out, k_out, q_weight, k_weight, \
-                       positions, a);                                                                                \
+#define DRIFT_QK_CASE(G)                                                                                     \
+  case G:                                                                                                    \
+    hipLaunchKernelGGL((qk_norm_rope_waves<T, G>), waves_grid, dim3(256), 0, st, q, k, q_out, k_out, q_weight, \
+                       k_weight, positions, a);                                                              \
     break;
       DRIFT_QK_CASE(1)
       DRIFT_QK_CASE(2)
