@@ -51,56 +51,116 @@ __device__ __forceinline__ void store8<float>(float* p, const float (&v)[8]) {
   *reinterpret_cast<float4*>(p + 4) = make_float4(v[4], v[5], v[6], v[7]);
 }
 
+// Work items are (id, segment of up to 128 blocks). A wave stages an item's
+// bytes with loads issued back to back (indices clamped, not branched, so no
+// load waits on the one before), writes them to its LDS slice, starts the
+// loads of its next item, then decodes and stores this one.
+template <bool ALIGNED>
+struct Stage;
+
+template <>
+struct Stage<true> {  // 16-byte loads: a segment is at most 272 of them
+  static constexpr int kLoads = (kSegmentBytes / 16 + kWave - 1) / kWave;
+  uint4 q[kLoads];
+  __device__ __forceinline__ void load(const uint8_t* source, int bytes, int lane) {
+    const int n = bytes / 16;
+#pragma unroll
+    for (int k = 0; k < kLoads; ++k) q[k] = reinterpret_cast<const uint4*>(source)[min(k * kWave + lane, n - 1)];
+  }
+  __device__ __forceinline__ void store(uint4* slice, const uint8_t* source, int bytes, int lane) const {
+    const int n = bytes / 16;
+#pragma unroll
+    for (int k = 0; k < kLoads; ++k)
+      if (k * kWave + lane < n) slice[k * kWave + lane] = q[k];
+    // a partial segment's last bytes (fewer than 16, an even count)
+    const int tail = (bytes - n * 16) / 2;
+    if (lane < tail)
+      reinterpret_cast<uint16_t*>(slice)[n * 8 + lane] = reinterpret_cast<const uint16_t*>(source)[n * 8 + lane];
+  }
+};
+
+template <>
+struct Stage<false> {  // 2-byte loads for rows that are not 16-byte aligned
+  static constexpr int kLoads = (kSegmentBytes / 2 + kWave - 1) / kWave;
+  uint16_t h[kLoads];
+  __device__ __forceinline__ void load(const uint8_t* source, int bytes, int lane) {
+    const int n = bytes / 2;
+#pragma unroll
+    for (int k = 0; k < kLoads; ++k) h[k] = reinterpret_cast<const uint16_t*>(source)[min(k * kWave + lane, n - 1)];
+  }
+  __device__ __forceinline__ void store(uint4* slice, const uint8_t*, int bytes, int lane) const {
+    const int n = bytes / 2;
+#pragma unroll
+    for (int k = 0; k < kLoads; ++k)
+      if (k * kWave + lane < n) reinterpret_cast<uint16_t*>(slice)[k * kWave + lane] = h[k];
+  }
+};
+
 template <typename T, bool ALIGNED>
 __global__ void __launch_bounds__(256) q8_0_gather(const uint8_t* table, const int32_t* ids, T* out, int64_t count,
                                                    int64_t vocab, int cols, int32_t* bad_id) {
   __shared__ uint4 stage[4][kSegmentBytes / 16];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  uint8_t* bytes = reinterpret_cast<uint8_t*>(stage[wave]);
-  const uint16_t* halves = reinterpret_cast<const uint16_t*>(stage[wave]);
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  uint4* slice = stage[wave];
+  const uint16_t* halves = reinterpret_cast<const uint16_t*>(slice);
   const int blocks = cols / 32;
+  const int segments = (blocks + kSegmentBlocks - 1) / kSegmentBlocks;
   const int64_t row_bytes = (int64_t)blocks * 34;
-  for (int64_t t = (int64_t)blockIdx.x * 4 + wave; t < count; t += (int64_t)gridDim.x * 4) {
-    const int64_t id = ids[t];
-    T* target = out + t * cols;
-    if (id < 0 || id >= vocab) {
+  const int64_t items = count * segments;
+  const int64_t stride = (int64_t)gridDim.x * 4;
+  Stage<ALIGNED> st;
+  // an item: its id (negative when outside the table), first block, block count
+  auto locate = [&](int64_t item, int64_t& id, int& first, int& nb) {
+    const int64_t t = item / segments;
+    first = (int)(item % segments) * kSegmentBlocks;
+    nb = min(kSegmentBlocks, blocks - first);
+    id = ids[t];
+    if (id >= vocab) id = -1;
+  };
+  int64_t item = (int64_t)blockIdx.x * 4 + wave;
+  int64_t id = -1;
+  int first = 0, nb = 0;
+  if (item < items) {
+    locate(item, id, first, nb);
+    if (id >= 0) st.load(table + id * row_bytes + (int64_t)first * 34, nb * 34, lane);
+  }
+  for (; item < items; item += stride) {
+    const int64_t t = item / segments;
+    T* target = out + t * cols + (int64_t)first * 32;
+    const int64_t this_id = id;
+    const int this_nb = nb;
+    if (this_id >= 0) {
+      wave_sync();  // the previous item has been read from the slice
+      st.store(slice, table + this_id * row_bytes + (int64_t)first * 34, this_nb * 34, lane);
+      wave_sync();
+    }
+    // the next item's bytes load while this one decodes
+    if (item + stride < items) {
+      locate(item + stride, id, first, nb);
+      if (id >= 0) st.load(table + id * row_bytes + (int64_t)first * 34, nb * 34, lane);
+    }
+    if (this_id < 0) {
       const float zeros[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-      for (int c = lane; c < cols / 8; c += kWave) store8<T>(target + c * 8, zeros);
+      for (int q = lane; q < this_nb * 4; q += kWave) store8<T>(target + q * 8, zeros);
       if (bad_id && lane == 0) *bad_id = 1;
       continue;
     }
-    const uint8_t* row = table + id * row_bytes;
-    for (int first = 0; first < blocks; first += kSegmentBlocks) {
-      const int nb = min(kSegmentBlocks, blocks - first);
-      const int seg_bytes = nb * 34;
-      const uint8_t* source = row + (int64_t)first * 34;
-      wave_sync();  // the previous segment has been read
-      if constexpr (ALIGNED) {
-        const int n16 = seg_bytes / 16;
-        for (int i = lane; i < n16; i += kWave) stage[wave][i] = reinterpret_cast<const uint4*>(source)[i];
-        for (int i = n16 * 8 + lane; i < seg_bytes / 2; i += kWave)
-          reinterpret_cast<uint16_t*>(bytes)[i] = reinterpret_cast<const uint16_t*>(source)[i];
-      } else {
-        for (int i = lane; i < seg_bytes / 2; i += kWave)
-          reinterpret_cast<uint16_t*>(bytes)[i] = reinterpret_cast<const uint16_t*>(source)[i];
-      }
-      wave_sync();
-      // 8 values per step: block b = q / 4, its quarter q % 4
-      for (int q = lane; q < nb * 4; q += kWave) {
-        const int b = q >> 2, part = q & 3;
-        const uint32_t h = halves[b * 17];
-        const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)h);
-        const uint32_t nan_bits = ((h & 0x8000u) << 16) | 0x7fc00000u | ((h & 0x3ffu) << 13);
-        const bool special = (h & 0x7c00u) == 0x7c00u;
-        float v[8];
+    // 8 values per step: block b = q / 4, its quarter q % 4
+    for (int q = lane; q < this_nb * 4; q += kWave) {
+      const int b = q >> 2, part = q & 3;
+      const uint32_t h = halves[b * 17];
+      const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+      const uint32_t nan_bits = ((h & 0x8000u) << 16) | 0x7fc00000u | ((h & 0x3ffu) << 13);
+      const bool special = (h & 0x7c00u) == 0x7c00u;
+      float v[8];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const uint32_t pair = halves[b * 17 + 1 + part * 4 + i];
-          v[2 * i] = decode((int)(int8_t)(pair & 0xffu), d, special, nan_bits);
-          v[2 * i + 1] = decode((int)(int8_t)(pair >> 8), d, special, nan_bits);
-        }
-        store8<T>(target + (int64_t)first * 32 + q * 8, v);
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t pair = halves[b * 17 + 1 + part * 4 + i];
+        v[2 * i] = decode((int)(int8_t)(pair & 0xffu), d, special, nan_bits);
+        v[2 * i + 1] = decode((int)(int8_t)(pair >> 8), d, special, nan_bits);
       }
+      store8<T>(target + q * 8, v);
     }
   }
 }

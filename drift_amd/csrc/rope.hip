@@ -257,7 +257,7 @@ struct AxisTables {
   int64_t stride_mod;  // (blocks * waves) mod grid: a wave's step through the grid
 };
 
-template <typename T, bool FIXED>
+template <typename T, int K, bool FIXED>
 __global__ void __launch_bounds__(512) rope_3d_axes(const T* x, T* out, Rope3dArgs p, AxisTables at) {
   constexpr int N = Chunk<T>::N;
   using Raw = typename Chunk<T>::Raw;
@@ -283,67 +283,68 @@ __global__ void __launch_bounds__(512) rope_3d_axes(const T* x, T* out, Rope3dAr
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int waves = blockDim.x >> 6;
-  const int per_token = p.heads * p.dim / N;  // chunks of a token
+  const int per_token = p.heads * p.dim / N;  // chunks of a token, at most K * 64
   const int per_head = p.dim / N;
   const int64_t stride = (int64_t)gridDim.x * waves;
   int64_t t = (int64_t)blockIdx.x * waves + wave;
   int64_t g = (p.token_offset + t) % p.grid;
   const int plane = p.rows * p.cols;
-  constexpr int kMaxChunks = 8;  // per lane per token, in flight at once
-  const int rounds = (per_token + kMaxChunks * kWave - 1) / (kMaxChunks * kWave);
+  // loads are never branched around (a branch makes each wait for the one
+  // before): chunk indices past the token are clamped and their values unused
+  auto load_token = [&](int64_t token, Raw(&into)[K]) {
+    const T* xt = x + token * p.heads * p.dim;
+#pragma unroll
+    for (int k = 0; k < K; ++k) into[k] = Chunk<T>::load_raw(xt + min(k * kWave + lane, per_token - 1) * N);
+  };
+  Raw raw[K];
+  if (t < p.tokens) load_token(t, raw);
   for (; t < p.tokens; t += stride) {
+    Raw next[K];
+    if (t + stride < p.tokens) load_token(t + stride, next);
     const int frame = (int)(g / plane), rem = (int)(g % plane);
-    const int base[3] = {frame * p0, at.base1 + (rem / p.cols) * p1, at.base2 + (rem % p.cols) * p2};
-    const T* xt = x + t * p.heads * p.dim;
-    T* ot = out + t * p.heads * p.dim;
+    const int base0 = frame * p0, base1 = at.base1 + (rem / p.cols) * p1, base2 = at.base2 + (rem % p.cols) * p2;
+    auto entry = [&](int m) {
+      return m < p0 ? base0 + m : (m < p0 + p1 ? base1 + m - p0 : base2 + m - p0 - p1);
+    };
     // the lane's pairs' cos and sin, when they are the same in every chunk
     double fc[N / 2], fs[N / 2];
     if constexpr (FIXED) {
       const int d0 = (lane % per_head) * N;
 #pragma unroll
       for (int i = 0; i < N / 2; ++i) {
-        const int m = d0 / 2 + i;
-        const int e = m < p0 ? base[0] + m : (m < p0 + p1 ? base[1] + m - p0 : base[2] + m - p0 - p1);
-        const float2 q = axis_cs[e];
+        const float2 q = axis_cs[entry(d0 / 2 + i)];
         fc[i] = q.x;
         fs[i] = q.y;
       }
     }
-    for (int r = 0; r < rounds; ++r) {
-      Raw raw[kMaxChunks];
+    T* ot = out + t * p.heads * p.dim;
 #pragma unroll
-      for (int k = 0; k < kMaxChunks; ++k) {
-        const int q = (r * kMaxChunks + k) * kWave + lane;
-        if (q < per_token) raw[k] = Chunk<T>::load_raw(xt + q * N);
-      }
+    for (int k = 0; k < K; ++k) {
+      const int q = k * kWave + lane;
+      if (q < per_token) {
+        float v[N];
+        Chunk<T>::unpack(raw[k], v);
+        const int d0 = (q % per_head) * N;
 #pragma unroll
-      for (int k = 0; k < kMaxChunks; ++k) {
-        const int q = (r * kMaxChunks + k) * kWave + lane;
-        if (q < per_token) {
-          float v[N];
-          Chunk<T>::unpack(raw[k], v);
-          const int d0 = (q % per_head) * N;
-#pragma unroll
-          for (int i = 0; i < N / 2; ++i) {
-            double c, sn;
-            if constexpr (FIXED) {
-              c = fc[i];
-              sn = fs[i];
-            } else {
-              const int m = d0 / 2 + i;
-              const int e = m < p0 ? base[0] + m : (m < p0 + p1 ? base[1] + m - p0 : base[2] + m - p0 - p1);
-              const float2 cs = axis_cs[e];
-              c = cs.x;
-              sn = cs.y;
-            }
-            const double a = v[2 * i], b = v[2 * i + 1];
-            v[2 * i] = (float)fma(a, c, -(b * sn));
-            v[2 * i + 1] = (float)fma(a, sn, b * c);
+        for (int i = 0; i < N / 2; ++i) {
+          double c, sn;
+          if constexpr (FIXED) {
+            c = fc[i];
+            sn = fs[i];
+          } else {
+            const float2 cs = axis_cs[entry(d0 / 2 + i)];
+            c = cs.x;
+            sn = cs.y;
           }
-          Chunk<T>::store(ot + q * N, v);
+          const double a = v[2 * i], b = v[2 * i + 1];
+          v[2 * i] = (float)fma(a, c, -(b * sn));
+          v[2 * i + 1] = (float)fma(a, sn, b * c);
         }
+        Chunk<T>::store(ot + q * N, v);
       }
     }
+#pragma unroll
+    for (int k = 0; k < K; ++k) raw[k] = next[k];
     g += at.stride_mod;
     if (g >= p.grid) g -= p.grid;
   }
@@ -715,11 +716,24 @@ int rope_3d(const char* entry, const T* x, T* out, int64_t tokens, int32_t heads
     const unsigned blocks = (unsigned)std::min<int64_t>(ceil_div(tokens, waves), 512);
     at.stride_mod = ((int64_t)blocks * waves) % p.grid;
     const size_t lds = (size_t)entries * sizeof(float2);
-    if ((64 % (dim / N)) == 0)
-      hipLaunchKernelGGL((rope_3d_axes<T, true>), dim3(blocks), dim3(64 * waves), lds, st, x, out, p, at);
-    else
-      hipLaunchKernelGGL((rope_3d_axes<T, false>), dim3(blocks), dim3(64 * waves), lds, st, x, out, p, at);
-    return launched(entry);
+    const int per_lane = (int)ceil_div((int64_t)heads * dim / N, kWave);
+    const bool fixed = (64 % (dim / N)) == 0;
+#define DRIFT_ROPE3D_CASE(K)                                                                                  \
+  if (per_lane <= K) {                                                                                        \
+    if (fixed)                                                                                                \
+      hipLaunchKernelGGL((rope_3d_axes<T, K, true>), dim3(blocks), dim3(64 * waves), lds, st, x, out, p, at);  \
+    else                                                                                                      \
+      hipLaunchKernelGGL((rope_3d_axes<T, K, false>), dim3(blocks), dim3(64 * waves), lds, st, x, out, p, at); \
+    return launched(entry);                                                                                   \
+  }
+    DRIFT_ROPE3D_CASE(1)
+    DRIFT_ROPE3D_CASE(2)
+    DRIFT_ROPE3D_CASE(4)
+    DRIFT_ROPE3D_CASE(6)
+    DRIFT_ROPE3D_CASE(8)
+    DRIFT_ROPE3D_CASE(12)
+    DRIFT_ROPE3D_CASE(16)
+#undef DRIFT_ROPE3D_CASE
   }
   const dim3 grid(grid_for(tokens, 1, 1 << 16));
   if (chunked)
