@@ -231,6 +231,9 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU reference work, about")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="", help="comma-separated kernel names to run (profiling)")
+    ap.add_argument("--copy-reference", action="store_true",
+                    help="also run a plain 512 MiB device copy (torch copy_), the known-size kernel that "
+                         "rocprofv3's FETCH_SIZE and WRITE_SIZE are scaled by")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this path runs on one GPU; --gpus {args.gpus} is not supported "
@@ -243,6 +246,11 @@ def main():
     if args.only:
         keep = set(args.only.split(","))
         kernels = [k for k in kernels if k.name in keep]
+    if args.copy_reference:
+        src = torch.empty(256 << 20, dtype=torch.bfloat16, device=DEV).fill_(1.0)
+        dst = torch.empty_like(src)
+        kernels.append(Kernel("copy_reference", "plain device copy, 512 MiB read + 512 MiB written",
+                              2 * src.numel() * 2, src.numel(), lambda i: dst.copy_(src)))
     torch.cuda.synchronize()
 
     call = 0
@@ -272,6 +280,7 @@ def main():
     if not args.no_cpu:
         cpu_baseline(kernels, args.cpu_budget)
 
+    kernels = [k for k in kernels if k.name != "copy_reference"]
     step_bytes = sum(k.bytes for k in kernels)
     ms_per_step = wall * 1e3 / args.steps
     table = {}
