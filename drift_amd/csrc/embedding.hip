@@ -47,8 +47,8 @@ __device__ __forceinline__ void store8<uint16_t>(uint16_t* p, const float (&v)[8
 
 template <>
 __device__ __forceinline__ void store8<float>(float* p, const float (&v)[8]) {
-  *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
-  *reinterpret_cast<float4*>(p + 4) = make_float4(v[4], v[5], v[6], v[7]);
+  Chunk<float>::store(p, *reinterpret_cast<const float(*)[4]>(v));
+  Chunk<float>::store(p + 4, *reinterpret_cast<const float(*)[4]>(v + 4));
 }
 
 // Work items are (id, segment of up to 128 blocks). A wave stages an item's
@@ -146,19 +146,30 @@ __global__ void __launch_bounds__(256) q8_0_gather(const uint8_t* table, const i
       if (bad_id && lane == 0) *bad_id = 1;
       continue;
     }
-    // 8 values per step: block b = q / 4, its quarter q % 4
+    // 8 values per step: block b = q / 4, its quarter q % 4. Infinite and
+    // NaN scales take the slow path only in a wave that holds one.
     for (int q = lane; q < this_nb * 4; q += kWave) {
       const int b = q >> 2, part = q & 3;
       const uint32_t h = halves[b * 17];
       const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)h);
-      const uint32_t nan_bits = ((h & 0x8000u) << 16) | 0x7fc00000u | ((h & 0x3ffu) << 13);
       const bool special = (h & 0x7c00u) == 0x7c00u;
-      float v[8];
+      uint32_t pairs[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t pair = halves[b * 17 + 1 + part * 4 + i];
-        v[2 * i] = decode((int)(int8_t)(pair & 0xffu), d, special, nan_bits);
-        v[2 * i + 1] = decode((int)(int8_t)(pair >> 8), d, special, nan_bits);
+      for (int i = 0; i < 4; ++i) pairs[i] = halves[b * 17 + 1 + part * 4 + i];
+      float v[8];
+      if (__builtin_expect(__any(special), 0)) {
+        const uint32_t nan_bits = ((h & 0x8000u) << 16) | 0x7fc00000u | ((h & 0x3ffu) << 13);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          v[2 * i] = decode((int)(int8_t)(pairs[i] & 0xffu), d, special, nan_bits);
+          v[2 * i + 1] = decode((int)(int8_t)(pairs[i] >> 8), d, special, nan_bits);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          v[2 * i] = (float)(int8_t)(pairs[i] & 0xffu) * d;
+          v[2 * i + 1] = (float)(int8_t)(pairs[i] >> 8) * d;
+        }
       }
       store8<T>(target + q * 8, v);
     }

@@ -483,21 +483,45 @@ __global__ void __launch_bounds__(256) qk_norm_rope_chunks(const T* q, const T* 
 // then passes of 64 / G heads, G lanes per head each holding two chunks (NeoX:
 // a chunk and its partner; otherwise chunks i and i + G), every pass's loads
 // issued before the first pass computes.
-template <typename T, int G>
-__global__ void __launch_bounds__(256) qk_norm_rope_waves(const T* q, const T* k, T* q_out, T* k_out,
+//
+// LDS is laid out so the G lanes of a head read consecutive entries: for NeoX
+// the pair (and weight) of lane i0's value i sits at i * G + i0 (the natural
+// index would put the G lanes 128 bytes apart, on the same banks). Each pass
+// re-reads its angles and weights from LDS rather than keeping them in
+// registers, which keeps every token's wave resident in one round.
+template <bool NEOX, int G, int N>
+__device__ __forceinline__ int qk_pair_slot(int pair) {
+  if constexpr (NEOX) return (pair % N) * G + pair / N;
+  return pair;
+}
+
+template <bool NEOX, int G, int N>
+__device__ __forceinline__ int qk_weight_slot(int d) {
+  if constexpr (NEOX) {
+    const int half = N * G;
+    const int h = d >= half ? 1 : 0, e = d - h * half;
+    return h * half + (e % N) * G + e / N;
+  }
+  return d;
+}
+
+template <typename T, int G, bool NEOX>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) qk_norm_rope_waves(const T* q, const T* k, T* q_out, T* k_out,
                                                           const float* q_weight, const float* k_weight,
                                                           const int32_t* positions, QkArgs a) {
   constexpr int N = Chunk<T>::N;
   using Raw = typename Chunk<T>::Raw;
   constexpr int kHeadsPerPass = kWave / G;
-  constexpr int kMaxPasses = 4;
-  __shared__ double2 cs_all[4][kMaxPairs / 2];  // dim = 2 N G <= 2 N 64, pairs = N G
-  __shared__ double weights[2][2 * kMaxPairs];
+  constexpr int kMaxPasses = 5;
+  constexpr int kPairs = N * G;  // a head's pairs (rotary == dim == 2 N G)
+  __shared__ double2 cs_all[4][kPairs];
+  __shared__ double weights[2][2 * kPairs];
   const RopeArgs& p = a.rope;
   const int dim = 2 * N * G, half = N * G;
   for (int d = threadIdx.x; d < dim; d += blockDim.x) {
-    weights[0][d] = (double)q_weight[d] + (double)a.offset;
-    weights[1][d] = (double)k_weight[d] + (double)a.offset;
+    const int slot = qk_weight_slot<NEOX, G, N>(d);
+    weights[0][slot] = (double)q_weight[d] + (double)a.offset;
+    weights[1][slot] = (double)k_weight[d] + (double)a.offset;
   }
   __syncthreads();
   const int lane = threadIdx.x & 63;
@@ -512,7 +536,7 @@ __global__ void __launch_bounds__(256) qk_norm_rope_waves(const T* q, const T* k
       const int32_t position = positions[(int64_t)rope_section(j, p) * p.tokens + t];
       double sn, cn;
       sincos((double)((float)position * p.inverse[j]), &sn, &cn);
-      cs[j] = make_double2(cn, sn);
+      cs[qk_pair_slot<NEOX, G, N>(j)] = make_double2(cn, sn);
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -521,8 +545,9 @@ __global__ void __launch_bounds__(256) qk_norm_rope_waves(const T* q, const T* k
       Raw r0[kMaxPasses], r1[kMaxPasses];
 #pragma unroll
       for (int s = 0; s < kMaxPasses; ++s) {
-        const int h = (first + s) * kHeadsPerPass + lane / G;
-        if (first + s < passes && h < rows) {
+        if (first + s < passes) {
+          // a head past the last is clamped to it: loads are never branched around
+          const int h = min((first + s) * kHeadsPerPass + lane / G, rows - 1);
           const T* xh = h < a.q_heads ? q + (t * a.q_heads + h) * dim : k + (t * a.kv_heads + (h - a.q_heads)) * dim;
           r0[s] = Chunk<T>::load_raw(xh + d0);
           r1[s] = Chunk<T>::load_raw(xh + d1);
@@ -531,8 +556,8 @@ __global__ void __launch_bounds__(256) qk_norm_rope_waves(const T* q, const T* k
 #pragma unroll
       for (int s = 0; s < kMaxPasses; ++s) {
         if (first + s >= passes) break;
+        asm volatile("" ::: "memory");  // angles and weights are re-read from LDS each pass
         const int h = (first + s) * kHeadsPerPass + lane / G;
-        const bool live = h < rows;
         const bool query = h < a.q_heads;
         float v0[N], v1[N];
         Chunk<T>::unpack(r0[s], v0);
@@ -544,18 +569,18 @@ __global__ void __launch_bounds__(256) qk_norm_rope_waves(const T* q, const T* k
           squares = fma((double)v1[i], (double)v1[i], squares);
         }
         squares = group_sum<G>(squares);
-        if (live) {
+        if (h < rows) {
           const double factor = 1.0 / sqrt(squares / (double)dim + (double)a.eps);
           const double* w = weights[query ? 0 : 1];
 #pragma unroll
           for (int i = 0; i < N; ++i) {
-            v0[i] = (float)((double)v0[i] * factor * w[d0 + i]);
-            v1[i] = (float)((double)v1[i] * factor * w[d1 + i]);
+            v0[i] = (float)((double)v0[i] * factor * w[qk_weight_slot<NEOX, G, N>(d0 + i)]);
+            v1[i] = (float)((double)v1[i] * factor * w[qk_weight_slot<NEOX, G, N>(d1 + i)]);
           }
-          if (p.layout == DRIFT_ROPE_NEOX) {
+          if constexpr (NEOX) {
 #pragma unroll
             for (int i = 0; i < N; ++i) {
-              const double2 c = cs[d0 + i];
+              const double2 c = cs[qk_pair_slot<NEOX, G, N>(d0 + i)];
               turn_fused(v0[i], v1[i], c.x, c.y, v0[i], v1[i]);
             }
           } else {
@@ -771,10 +796,14 @@ int qk_norm_rope(const char* entry, const T* q, const T* k, T* q_out, T* k_out, 
   if (whole) {
     const dim3 waves_grid(grid_for(tokens, 4, 1 << 16));
     switch (lanes_per_head) {
-#define DRIFT_QK_CASE(G)                                                                                     \
-  case G:                                                                                                    \
-    hipLaunchKernelGGL((qk_norm_rope_waves<T, G>), waves_grid, dim3(256), 0, st, q, k, q_out, k_out, q_weight, \
-                       k_weight, positions, a);                                                              \
+#define DRIFT_QK_CASE(G)                                                                                    \
+  case G:                                                                                                   \
+    if (layout == DRIFT_ROPE_NEOX)                                                                          \
+      hipLaunchKernelGGL((qk_norm_rope_waves<T, G, true>), waves_grid, dim3(256), 0, st, q, k, q_out, k_out,  \
+                         q_weight, k_weight, positions, a);                                                 \
+    else                                                                                                    \
+      hipLaunchKernelGGL((qk_norm_rope_waves<T, G, false>), waves_grid, dim3(256), 0, st, q, k, q_out, k_out, \
+                         q_weight, k_weight, positions, a);                                                 \
     break;
       DRIFT_QK_CASE(1)
       DRIFT_QK_CASE(2)
