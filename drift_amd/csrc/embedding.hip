@@ -6,25 +6,25 @@
 // which is exact in float (11-bit by 8-bit significands), so the BF16 output
 // is bit-exact against the reference's F32 gather rounded to BF16.
 //
-// One wave per id. A row is walked in segments of 128 blocks (4352 bytes,
-// 4096 values): the wave stages the segment in its slice of LDS with 16-byte
-// loads (34-byte blocks are only 2-byte aligned), then each lane decodes
-// 8 consecutive values per step from LDS and stores them as one 16-byte
-// (BF16) or two 16-byte (F32) writes; a store instruction of the wave covers
-// a contiguous 1 or 2 KiB of the output row.
+// One wave per id. A lane owns chunks of 8 consecutive values (a quarter of a
+// block): it loads the chunk's 8 codes and the block's scale straight from the
+// table row, decodes them and stores them as one 16-byte (BF16) or two 16-byte
+// (F32) writes, so a store instruction of the wave covers a contiguous 1 or
+// 2 KiB of the output row. Eight chunks per lane are loaded back to back
+// (indices clamped, not branched, so no load waits on another) before any is
+// decoded: a wave has 4096 values of one row in flight.
+//
+// Codes sit at 2-byte offsets (34-byte blocks). When rows start on 4-byte
+// boundaries (an even number of blocks per row and a 4-byte aligned table) a
+// chunk's 8 codes are read as one 12-byte window from the 4-byte boundary at
+// or below them, clamped to end at the row's end, and shifted into place;
+// otherwise they are read as four 2-byte loads.
 #include "common.hpp"
 
 namespace drift {
 namespace {
 
-constexpr int kSegmentBlocks = 128;
-constexpr int kSegmentBytes = kSegmentBlocks * 34;  // 4352, a multiple of 16
-
-__device__ __forceinline__ void wave_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
+constexpr int kChunksPerLane = 8;
 
 // float(code) * d as the reference computes it on x86: exact for finite d; an
 // infinite d times code 0 is the x86 default NaN; a NaN d comes back as the
@@ -51,127 +51,96 @@ __device__ __forceinline__ void store8<float>(float* p, const float (&v)[8]) {
   Chunk<float>::store(p + 4, *reinterpret_cast<const float(*)[4]>(v + 4));
 }
 
-// Work items are (id, segment of up to 128 blocks). A wave stages an item's
-// bytes with loads issued back to back (indices clamped, not branched, so no
-// load waits on the one before), writes them to its LDS slice, starts the
-// loads of its next item, then decodes and stores this one.
-template <bool ALIGNED>
-struct Stage;
+// The 8 codes of chunk q (block q / 4, quarter q % 4) of a row, as raw bytes
+// in two words, little-endian.
+template <bool WORDS>
+struct Codes;
 
 template <>
-struct Stage<true> {  // 16-byte loads: a segment is at most 272 of them
-  static constexpr int kLoads = (kSegmentBytes / 16 + kWave - 1) / kWave;
-  uint4 q[kLoads];
-  __device__ __forceinline__ void load(const uint8_t* source, int bytes, int lane) {
-    const int n = bytes / 16;
-#pragma unroll
-    for (int k = 0; k < kLoads; ++k) q[k] = reinterpret_cast<const uint4*>(source)[min(k * kWave + lane, n - 1)];
+struct Codes<true> {  // rows on 4-byte boundaries: one 12-byte window
+  uint3 w;
+  uint32_t offset;  // 0, 2 or 4: where the codes start in the window
+  __device__ __forceinline__ void load(const uint8_t* row, int64_t row_bytes, int q) {
+    const int64_t at = (int64_t)(q >> 2) * 34 + 2 + (q & 3) * 8;
+    const int64_t base = min(at & ~(int64_t)3, row_bytes - 12);
+    offset = (uint32_t)(at - base);
+    w = *reinterpret_cast<const uint3*>(row + base);
   }
-  __device__ __forceinline__ void store(uint4* slice, const uint8_t* source, int bytes, int lane) const {
-    const int n = bytes / 16;
-#pragma unroll
-    for (int k = 0; k < kLoads; ++k)
-      if (k * kWave + lane < n) slice[k * kWave + lane] = q[k];
-    // a partial segment's last bytes (fewer than 16, an even count)
-    const int tail = (bytes - n * 16) / 2;
-    if (lane < tail)
-      reinterpret_cast<uint16_t*>(slice)[n * 8 + lane] = reinterpret_cast<const uint16_t*>(source)[n * 8 + lane];
+  __device__ __forceinline__ void words(uint32_t& lo, uint32_t& hi) const {
+    lo = offset == 4 ? w.y : __builtin_amdgcn_alignbyte(w.y, w.x, offset);
+    hi = offset == 4 ? w.z : __builtin_amdgcn_alignbyte(w.z, w.y, offset);
   }
 };
 
 template <>
-struct Stage<false> {  // 2-byte loads for rows that are not 16-byte aligned
-  static constexpr int kLoads = (kSegmentBytes / 2 + kWave - 1) / kWave;
-  uint16_t h[kLoads];
-  __device__ __forceinline__ void load(const uint8_t* source, int bytes, int lane) {
-    const int n = bytes / 2;
+struct Codes<false> {  // rows on 2-byte boundaries: four 2-byte loads
+  uint16_t h[4];
+  __device__ __forceinline__ void load(const uint8_t* row, int64_t, int q) {
+    const uint16_t* codes = reinterpret_cast<const uint16_t*>(row + (int64_t)(q >> 2) * 34 + 2 + (q & 3) * 8);
 #pragma unroll
-    for (int k = 0; k < kLoads; ++k) h[k] = reinterpret_cast<const uint16_t*>(source)[min(k * kWave + lane, n - 1)];
+    for (int i = 0; i < 4; ++i) h[i] = codes[i];
   }
-  __device__ __forceinline__ void store(uint4* slice, const uint8_t*, int bytes, int lane) const {
-    const int n = bytes / 2;
-#pragma unroll
-    for (int k = 0; k < kLoads; ++k)
-      if (k * kWave + lane < n) reinterpret_cast<uint16_t*>(slice)[k * kWave + lane] = h[k];
+  __device__ __forceinline__ void words(uint32_t& lo, uint32_t& hi) const {
+    lo = h[0] | ((uint32_t)h[1] << 16);
+    hi = h[2] | ((uint32_t)h[3] << 16);
   }
 };
 
-template <typename T, bool ALIGNED>
+template <typename T, bool WORDS>
 __global__ void __launch_bounds__(256) q8_0_gather(const uint8_t* table, const int32_t* ids, T* out, int64_t count,
                                                    int64_t vocab, int cols, int32_t* bad_id) {
-  __shared__ uint4 stage[4][kSegmentBytes / 16];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  uint4* slice = stage[wave];
-  const uint16_t* halves = reinterpret_cast<const uint16_t*>(slice);
   const int blocks = cols / 32;
-  const int segments = (blocks + kSegmentBlocks - 1) / kSegmentBlocks;
+  const int chunks = blocks * 4;
   const int64_t row_bytes = (int64_t)blocks * 34;
-  const int64_t items = count * segments;
-  const int64_t stride = (int64_t)gridDim.x * 4;
-  Stage<ALIGNED> st;
-  // an item: its id (negative when outside the table), first block, block count
-  auto locate = [&](int64_t item, int64_t& id, int& first, int& nb) {
-    const int64_t t = item / segments;
-    first = (int)(item % segments) * kSegmentBlocks;
-    nb = min(kSegmentBlocks, blocks - first);
-    id = ids[t];
-    if (id >= vocab) id = -1;
-  };
-  int64_t item = (int64_t)blockIdx.x * 4 + wave;
-  int64_t id = -1;
-  int first = 0, nb = 0;
-  if (item < items) {
-    locate(item, id, first, nb);
-    if (id >= 0) st.load(table + id * row_bytes + (int64_t)first * 34, nb * 34, lane);
-  }
-  for (; item < items; item += stride) {
-    const int64_t t = item / segments;
-    T* target = out + t * cols + (int64_t)first * 32;
-    const int64_t this_id = id;
-    const int this_nb = nb;
-    if (this_id >= 0) {
-      wave_sync();  // the previous item has been read from the slice
-      st.store(slice, table + this_id * row_bytes + (int64_t)first * 34, this_nb * 34, lane);
-      wave_sync();
-    }
-    // the next item's bytes load while this one decodes
-    if (item + stride < items) {
-      locate(item + stride, id, first, nb);
-      if (id >= 0) st.load(table + id * row_bytes + (int64_t)first * 34, nb * 34, lane);
-    }
-    if (this_id < 0) {
+  for (int64_t t = (int64_t)blockIdx.x * 4 + wave; t < count; t += (int64_t)gridDim.x * 4) {
+    const int64_t id = ids[t];
+    T* target = out + t * cols;
+    if (id < 0 || id >= vocab) {
       const float zeros[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-      for (int q = lane; q < this_nb * 4; q += kWave) store8<T>(target + q * 8, zeros);
+      for (int q = lane; q < chunks; q += kWave) store8<T>(target + q * 8, zeros);
       if (bad_id && lane == 0) *bad_id = 1;
       continue;
     }
-    // 8 values per step: block b = q / 4, its quarter q % 4. Infinite and
-    // NaN scales take the slow path only in a wave that holds one.
-    for (int q = lane; q < this_nb * 4; q += kWave) {
-      const int b = q >> 2, part = q & 3;
-      const uint32_t h = halves[b * 17];
-      const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)h);
-      const bool special = (h & 0x7c00u) == 0x7c00u;
-      uint32_t pairs[4];
+    const uint8_t* row = table + id * row_bytes;
+    for (int first = 0; first < chunks; first += kChunksPerLane * kWave) {
+      Codes<WORDS> codes[kChunksPerLane];
+      uint32_t scale[kChunksPerLane];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) pairs[i] = halves[b * 17 + 1 + part * 4 + i];
-      float v[8];
-      if (__builtin_expect(__any(special), 0)) {
-        const uint32_t nan_bits = ((h & 0x8000u) << 16) | 0x7fc00000u | ((h & 0x3ffu) << 13);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          v[2 * i] = decode((int)(int8_t)(pairs[i] & 0xffu), d, special, nan_bits);
-          v[2 * i + 1] = decode((int)(int8_t)(pairs[i] >> 8), d, special, nan_bits);
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          v[2 * i] = (float)(int8_t)(pairs[i] & 0xffu) * d;
-          v[2 * i + 1] = (float)(int8_t)(pairs[i] >> 8) * d;
-        }
+      for (int k = 0; k < kChunksPerLane; ++k) {
+        const int q = min(first + k * kWave + lane, chunks - 1);
+        codes[k].load(row, row_bytes, q);
+        scale[k] = *reinterpret_cast<const uint16_t*>(row + (int64_t)(q >> 2) * 34);
       }
-      store8<T>(target + q * 8, v);
+#pragma unroll
+      for (int k = 0; k < kChunksPerLane; ++k) {
+        const int q = first + k * kWave + lane;
+        if (q >= chunks) break;
+        uint32_t lo, hi;
+        codes[k].words(lo, hi);
+        const uint32_t h = scale[k];
+        const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+        const bool special = (h & 0x7c00u) == 0x7c00u;
+        const uint32_t pairs[4] = {lo & 0xffffu, lo >> 16, hi & 0xffffu, hi >> 16};
+        float v[8];
+        // infinite and NaN scales take the slow path only in a wave that holds one
+        if (__builtin_expect(__any(special), 0)) {
+          const uint32_t nan_bits = ((h & 0x8000u) << 16) | 0x7fc00000u | ((h & 0x3ffu) << 13);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            v[2 * i] = decode((int)(int8_t)(pairs[i] & 0xffu), d, special, nan_bits);
+            v[2 * i + 1] = decode((int)(int8_t)(pairs[i] >> 8), d, special, nan_bits);
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            v[2 * i] = (float)(int8_t)(pairs[i] & 0xffu) * d;
+            v[2 * i + 1] = (float)(int8_t)(pairs[i] >> 8) * d;
+          }
+        }
+        store8<T>(target + q * 8, v);
+      }
     }
   }
 }
@@ -185,11 +154,12 @@ int embedding_q8_0(const char* entry, const uint8_t* table, const int32_t* ids, 
   if (count == 0) return 0;
   if (!table || !ids || !out) return refuse("%s: null table, ids or out", entry);
   if (!aligned16(out)) return refuse("%s: out is not 16-byte aligned", entry);
+  if (reinterpret_cast<uintptr_t>(table) & 1u) return refuse("%s: table is not 2-byte aligned", entry);
   const int64_t row_bytes = (int64_t)cols / 32 * 34;
-  const bool aligned = aligned16(table) && row_bytes % 16 == 0;
+  const bool words = (reinterpret_cast<uintptr_t>(table) & 3u) == 0 && row_bytes % 4 == 0;
   const dim3 grid(grid_for(count, 4, 1 << 16));
   const hipStream_t s = (hipStream_t)stream;
-  if (aligned)
+  if (words)
     hipLaunchKernelGGL((q8_0_gather<T, true>), grid, dim3(256), 0, s, table, ids, out, count, vocab, cols, bad_id);
   else
     hipLaunchKernelGGL((q8_0_gather<T, false>), grid, dim3(256), 0, s, table, ids, out, count, vocab, cols, bad_id);

@@ -284,8 +284,6 @@ __global__ void __launch_bounds__(512) adaln_rows(const T* x, const float* scale
   };
   if (row < end) load_row(row, raw);
   for (; row < end; row += stride) {
-    Raw next[K];
-    if (row + stride < end) load_row(row + stride, next);  // in flight while this row computes
     float first_value[N];
     Chunk<T>::unpack(raw[0], first_value);
     const double x0 = (double)__shfl(first_value[0], 0);
@@ -326,8 +324,7 @@ __global__ void __launch_bounds__(512) adaln_rows(const T* x, const float* scale
         Chunk<T>::store(out + row * cols + c * N, o);
       }
     }
-#pragma unroll
-    for (int k = 0; k < K; ++k) raw[k] = next[k];
+    if (row + stride < end) load_row(row + stride, raw);
   }
 }
 

@@ -532,15 +532,6 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) q
   const int i0 = lane % G;
   const int d0 = i0 * N, d1 = half + i0 * N;
   for (int64_t t = (int64_t)blockIdx.x * 4 + wave; t < p.tokens; t += (int64_t)gridDim.x * 4) {
-    for (int j = lane; j < half; j += kWave) {
-      const int32_t position = positions[(int64_t)rope_section(j, p) * p.tokens + t];
-      double sn, cn;
-      sincos((double)((float)position * p.inverse[j]), &sn, &cn);
-      cs[qk_pair_slot<NEOX, G, N>(j)] = make_double2(cn, sn);
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     for (int first = 0; first < passes; first += kMaxPasses) {
       Raw r0[kMaxPasses], r1[kMaxPasses];
 #pragma unroll
@@ -552,6 +543,18 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) q
           r0[s] = Chunk<T>::load_raw(xh + d0);
           r1[s] = Chunk<T>::load_raw(xh + d1);
         }
+      }
+      if (first == 0) {
+        // the token's angles, made while its heads load
+        for (int j = lane; j < half; j += kWave) {
+          const int32_t position = positions[(int64_t)rope_section(j, p) * p.tokens + t];
+          double sn, cn;
+          sincos((double)((float)position * p.inverse[j]), &sn, &cn);
+          cs[qk_pair_slot<NEOX, G, N>(j)] = make_double2(cn, sn);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
       }
 #pragma unroll
       for (int s = 0; s < kMaxPasses; ++s) {
@@ -738,7 +741,7 @@ int rope_3d(const char* entry, const T* x, T* out, int64_t tokens, int32_t heads
     at.base2 = at.base1 + rows * axes[1];
     at.entries = (int32_t)entries;
     const int waves = 8;
-    const unsigned blocks = (unsigned)std::min<int64_t>(ceil_div(tokens, waves), 512);
+    const unsigned blocks = (unsigned)std::min<int64_t>(ceil_div(tokens, waves), 2048);
     at.stride_mod = ((int64_t)blocks * waves) % p.grid;
     const size_t lds = (size_t)entries * sizeof(float2);
     const int per_lane = (int)ceil_div((int64_t)heads * dim / N, kWave);
@@ -789,7 +792,7 @@ int qk_norm_rope(const char* entry, const T* q, const T* k, T* q_out, T* k_out, 
   constexpr int N = Chunk<T>::N;
   const int lanes_per_head = dim / (2 * N);
   const bool whole = rotary == dim && dim % (2 * N) == 0 && (lanes_per_head & (lanes_per_head - 1)) == 0 &&
-                     lanes_per_head <= kWave && (!q || (aligned16(q) && aligned16(q_out))) &&
+                     lanes_per_head <= kWave / 2 && (!q || (aligned16(q) && aligned16(q_out))) &&
                      (!k || (aligned16(k) && aligned16(k_out)));
   const dim3 grid(grid_for(tokens, 1, 1 << 16));
   const hipStream_t st = (hipStream_t)stream;
@@ -811,7 +814,6 @@ int qk_norm_rope(const char* entry, const T* q, const T* k, T* q_out, T* k_out, 
       DRIFT_QK_CASE(8)
       DRIFT_QK_CASE(16)
       DRIFT_QK_CASE(32)
-      DRIFT_QK_CASE(64)
 #undef DRIFT_QK_CASE
       default:
         return refuse("%s: no kernel for heads of %d values", entry, dim);

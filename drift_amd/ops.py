@@ -388,6 +388,7 @@ class HipOps:
         _require(cols % 32 == 0, f"{cols} elements are not whole Q8_0 blocks of 32")
         _require(tuple(table.data.shape) == (vocab, cols // 32 * 34) and table.data.dtype == torch.uint8,
                  f"embedding: Q8_0 bytes {_shape(table.data)} for rows of {cols}")
+        _require(table.data.is_contiguous(), "embedding: Q8_0 bytes must be contiguous rows")
         _on_device("embedding", table.data, ids, out)
         self._launch(f"drift_embedding_q8_0_{_suffix(out.dtype)}", _ptr(table.data), _ptr(ids), _ptr(out),
                      ids.shape[0], vocab, cols, _ptr(badId))

@@ -89,6 +89,12 @@ def _ptr(a: np.ndarray | None):
     return None if a is None else a.ctypes.data
 
 
+def _need(condition: bool, message: str) -> None:
+    """Shapes are checked here, before the C loops index the arrays."""
+    if not condition:
+        raise ValueError(message)
+
+
 def _c(a, dtype) -> np.ndarray:
     return np.ascontiguousarray(a, dtype=dtype)
 
@@ -145,7 +151,7 @@ def activation(kind: int, x, input_scale: float = 1.0) -> np.ndarray:
 
 def gated(kind: int, gate, up) -> np.ndarray:
     gate, up = _c(gate, np.float32), _c(up, np.float32)
-    assert gate.shape == up.shape
+    _need(gate.shape == up.shape, f"gated: gate {gate.shape}, up {up.shape}")
     out = np.empty_like(gate)
     lib().oracle_gated(kind, _ptr(gate), _ptr(up), _ptr(out), gate.size)
     return out
@@ -158,6 +164,9 @@ def rms_norm(x, weight, eps: float, offset: float = 0.0, y=None, weight_rows: in
     cols = x.shape[-1]
     rows = x.size // cols if cols else 0
     yy = None if y is None else _c(y, np.float32)
+    _need(weight.size == weight_rows * cols, f"rms_norm: weight of {weight.size} for {weight_rows} rows of {cols}")
+    _need(weight_rows >= 1 and rows % weight_rows == 0, f"rms_norm: {rows} rows in groups of {weight_rows}")
+    _need(yy is None or yy.shape == x.shape, "rms_norm: y is not x's shape")
     out = np.empty_like(x)
     lib().oracle_rms_norm(_ptr(x), _ptr(yy), _ptr(weight), _ptr(out), rows, cols, eps, offset, weight_rows)
     return out if y is None else (x, out)
@@ -168,6 +177,7 @@ def layer_norm(x, weight=None, bias=None, eps: float = 1e-5) -> np.ndarray:
     w = None if weight is None else _c(weight, np.float32)
     b = None if bias is None else _c(bias, np.float32)
     cols = x.shape[-1]
+    _need(all(v is None or v.size == cols for v in (w, b)), f"layer_norm: weight or bias not of {cols}")
     out = np.empty_like(x)
     lib().oracle_layer_norm(_ptr(x), _ptr(w), _ptr(b), _ptr(out), x.size // cols, cols, eps)
     return out
@@ -177,6 +187,7 @@ def modulate(x, scale, shift) -> np.ndarray:
     x = _c(x, np.float32)
     scale, shift = _c(scale, np.float32), _c(shift, np.float32)
     cols = x.shape[-1]
+    _need(scale.size == cols and shift.size == cols, f"modulate: scale or shift not of {cols}")
     out = np.empty_like(x)
     lib().oracle_modulate(_ptr(x), _ptr(scale), _ptr(shift), _ptr(out), x.size // cols, cols)
     return out
@@ -192,6 +203,10 @@ def rope(x, positions, theta: float, rotary: int, layout: int = NEOX, sections: 
     x = _c(x, np.float32)
     positions = _c(positions, np.int32)
     tokens, heads, dim = x.shape
+    _need(rotary % 2 == 0 and 0 < rotary <= dim, f"rope: {rotary} rotary dimensions of {dim}")
+    axes = {SINGLE: 1, CONTIGUOUS: 3, INTERLEAVED_MROPE: 3, AXES: len(sizes)}[sections]
+    _need(sections != AXES or 2 * sum(sizes) >= rotary, f"rope: axes {tuple(sizes)} cover fewer than {rotary} dims")
+    _need(positions.size >= axes * tokens, f"rope: {positions.size} positions for {axes} x {tokens} tokens")
     out = np.empty_like(x)
     lib().oracle_rope(_ptr(x), _ptr(positions), _ptr(out), tokens, heads, dim, rotary, theta, layout,
                       sections, _ptr(_sections(sizes)))
@@ -208,6 +223,10 @@ def rope_table(x, cosines, sines, halves: bool = False) -> np.ndarray:
     tokens, heads, dim = x.shape
     pairs = cosines.shape[-1]
     per_head = 1 if cosines.ndim == 3 else 0
+    want = (tokens, heads, pairs) if per_head else (tokens, pairs)
+    _need(cosines.shape == want and sines.shape == want,
+          f"rope_table: tables {cosines.shape} and {sines.shape} for x {x.shape} (want {want})")
+    _need(2 * pairs <= dim, f"rope_table: {pairs} pairs in heads of {dim}")
     out = np.empty_like(x)
     lib().oracle_rope_table(_ptr(x), _ptr(cosines), _ptr(sines), _ptr(out), tokens, heads, dim, pairs, per_head,
                             1 if halves else 0)
@@ -231,7 +250,8 @@ def wan_angles(frames: int, rows: int, cols: int, head_dim: int = 128, theta: fl
 def embedding_q8_0(table, vocab: int, cols: int, ids) -> np.ndarray:
     table = _c(table, np.uint8)
     ids = _c(ids, np.int32)
-    assert table.size == vocab * cols // 32 * 34
+    _need(cols % 32 == 0 and table.size == vocab * cols // 32 * 34,
+          f"embedding_q8_0: {table.size} bytes for {vocab} rows of {cols}")
     out = np.empty((ids.size, cols), np.float32)
     bad = lib().oracle_embedding_q8_0(_ptr(table), vocab, cols, _ptr(ids), ids.size, _ptr(out))
     if bad >= 0:

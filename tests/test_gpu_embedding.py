@@ -1,6 +1,6 @@
 """The Q8_0 embedding gather on the GPU: bit-exact against the oracle, F32 and
-BF16 outputs, every code and scale class, ids refused by the reference, and
-rows whose 34-byte blocks are not 16-byte aligned.
+BF16 outputs, every code and scale class, ids refused by the reference, rows
+of an odd number of blocks (2-byte aligned) and tables at a 2-byte offset.
 
 The reference has no GPU test of this gather (SmallOpsTests covers F32 tables
 only, OpsComparisonCoverageTests.scala:102-123), and its gguf-py golden for
@@ -13,6 +13,7 @@ import torch
 
 from drift_amd import ops as d
 from oracle import oracle as o
+from drift_amd import _lib
 from tests.helpers import DEV, assert_bits, dev_i32, host_bits, host_f32, step
 
 pytestmark = pytest.mark.gpu
@@ -28,7 +29,7 @@ def table_on_device(table, cols):
 
 
 @pytest.mark.parametrize("vocab,cols,count", [(2048, 4096, 300), (100, 32, 50), (300, 96, 77), (64, 8192, 9),
-                                              (50, 4160, 13), (10, 256, 1)])
+                                              (50, 4160, 13), (10, 256, 1), (40, 8192 + 96, 70)])
 def test_gather_matches_oracle_bit_for_bit(hip, vocab, cols, count):
     rng = np.random.default_rng(vocab + cols)
     table = o.q8_0_table(vocab, cols, rng)
@@ -88,3 +89,27 @@ def test_ids_outside_the_table(hip):
     flag.zero_()
     hip.embedding(table_on_device(table, 128), dev_i32(ids[good]), out[:3], badId=flag)
     assert int(flag.item()) == 0
+
+
+def test_table_at_a_two_byte_offset(hip):
+    # the bytes of a mapped table need not start on a 4-byte boundary
+    rng = np.random.default_rng(11)
+    vocab, cols = 97, 4096
+    table = o.q8_0_table(vocab, cols, rng)
+    flat = torch.zeros(table.size + 2, dtype=torch.uint8, device=DEV)
+    shifted = flat[2:].view(vocab, -1)
+    shifted.copy_(torch.from_numpy(table).to(DEV))
+    assert shifted.data_ptr() % 4 == 2
+    ids = rng.integers(0, vocab, 200).astype(np.int32)
+    want = o.embedding_q8_0(table, vocab, cols, ids)
+    step("Q8_0 gather, table at a 2-byte offset")
+    outb = torch.empty((200, cols), dtype=torch.bfloat16, device=DEV)
+    hip.embedding(d.Q8_0Table(shifted, cols), dev_i32(ids), outb)
+    assert_bits(o.to_bf16(want), host_bits(outb), what="bf16 shifted table")
+
+
+def test_table_at_an_odd_address_is_refused(hip):
+    flat = torch.zeros(34 * 4 + 1, dtype=torch.uint8, device=DEV)
+    out = torch.empty((1, 32), dtype=torch.float32, device=DEV)
+    with pytest.raises(_lib.HipError, match="2-byte aligned"):
+        hip.embedding(d.Q8_0Table(flat[1:].view(4, 34), 32), dev_i32(np.zeros(1, np.int32)), out)
