@@ -194,7 +194,8 @@ int drift_qk_norm_rope_bf16(const uint16_t* q, const uint16_t* k, uint16_t* q_ou
  * values a 34-byte block, fp16 scale d then 32 int8 codes), decoded as
  * float(code) * d (exact in F32), into out [count, cols]. An id outside
  * [0, vocab) gets a row of zeros and, when `bad_id` (device int32, nullable)
- * is given, sets *bad_id = 1; the CPU reference refuses such an id.
+ * is given, sets *bad_id = 1; the CPU reference refuses such an id. The
+ * table must be 2-byte aligned and `out` 16-byte aligned.
  * Replaces kernels/matvec.hip:830-839,894-897 gather_q8_0
  * (ops/HipLinear.scala:21-52; CPU ops/CpuLinear.scala:12-41 with
  * tensor/GgmlQuants.scala:104-118). BF16 output is bit-exact against
