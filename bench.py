@@ -2,6 +2,8 @@
 
 A step is one pass of the path over its configurations, every kernel once:
   C2  decode bf16: RMSNorm [B, 4096] and SwiGLU [B, 14336], B = 1, 8, 64
+      decode F32 with the int8 side output the products read: RMSNorm
+      [B, 4096] and SwiGLU [B, 14336], B = 1, 64
   C3  prefill bf16: per-head RMSNorm + NeoX RoPE, Q [4096, 32, 128], K [4096, 8, 128]
   C4  Q8_0 gather of 8192 ids from [151936, 4096] to bf16
   C5  Video DiT block bf16: AdaLN [65520, 3072], GELU-tanh in place, 3-D RoPE
@@ -28,6 +30,7 @@ work on this host's cores, scaled to the whole step.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import faulthandler
 import json
 import math
@@ -114,6 +117,23 @@ def randn_bf16(shape, seed, scale=1.0):
     return (scale * torch.randn(shape, generator=gen(seed), device=DEV)).to(torch.bfloat16)
 
 
+def _side(side, values):
+    """Pointers to the codes, scales and sums of a side-output buffer."""
+    base = side.data_ptr()
+    return (ctypes.c_void_p(base), ctypes.c_void_p(base + values), ctypes.c_void_p(base + values + 4 * (values // 32)))
+
+
+def side_args(x, y, w, out, rows, cols, side):
+    return (ctypes.c_void_p(x.data_ptr()), None if y is None else ctypes.c_void_p(y.data_ptr()),
+            ctypes.c_void_p(w.data_ptr()), ctypes.c_void_p(out.data_ptr()), rows, cols, 1e-5, 0.0, 1,
+            *_side(side, rows * cols))
+
+
+def gated_side_args(g, u, out, n, side):
+    return (ctypes.c_void_p(g.data_ptr()), ctypes.c_void_p(u.data_ptr()), ctypes.c_void_p(out.data_ptr()), n, 0,
+            *_side(side, n))
+
+
 def make_kernels(hip: d.HipOps):
     kernels = []
 
@@ -136,6 +156,32 @@ def make_kernels(hip: d.HipOps):
                               lambda i, gs=gs, us=us, os_=os_: hip.gated(d.Activation.Silu, gs[i % len(gs)],
                                                                          us[i % len(us)], os_[i % len(os_)]),
                               sets=n))
+
+    # The int8 side output for the decode products: F32 RMSNorm [B, 4096] and
+    # SwiGLU [B, 14336] writing their output quantized too (codes 1 B per
+    # value, scale and code sum 8 B per 32 values)
+    for b in (1, 64):
+        n = sets_for(b * 4096 * 9, 8, 8)
+        xs = [(0.5 * torch.randn((b, 4096), generator=gen(800 + i), device=DEV)) for i in range(n)]
+        outs = [torch.empty_like(xs[0]) for _ in range(n)]
+        sides = [torch.empty(b * 4096 + 8 * (b * 4096 // 32), dtype=torch.int8, device=DEV) for _ in range(n)]
+        w = (1 + 0.1 * torch.randn(4096, generator=gen(7), device=DEV)).float()
+        nbytes = b * 4096 * (4 + 4 + 1) + 8 * (b * 4096 // 32) + 4096 * 4
+        kernels.append(Kernel(f"rms_norm_q8_f32_b{b}", f"RMSNorm f32 [{b},4096] + int8 side output", nbytes, b,
+                              lambda i, xs=xs, outs=outs, sides=sides, w=w, b=b: hip._launch(
+                                  "drift_rms_norm_f32", *side_args(xs[i % len(xs)], None, w, outs[i % len(outs)], b,
+                                                                   4096, sides[i % len(sides)])), sets=n))
+        n = sets_for(b * 14336 * 13, 8, 8)
+        gs = [(0.5 * torch.randn((b, 14336), generator=gen(900 + i), device=DEV)) for i in range(n)]
+        us = [(0.5 * torch.randn((b, 14336), generator=gen(950 + i), device=DEV)) for i in range(n)]
+        os_ = [torch.empty_like(gs[0]) for _ in range(n)]
+        sides = [torch.empty(b * 14336 + 8 * (b * 14336 // 32), dtype=torch.int8, device=DEV) for _ in range(n)]
+        nbytes = b * 14336 * (4 + 4 + 4 + 1) + 8 * (b * 14336 // 32)
+        kernels.append(Kernel(f"swiglu_q8_f32_b{b}", f"SwiGLU f32 [{b},14336] + int8 side output", nbytes, b,
+                              lambda i, gs=gs, us=us, os_=os_, sides=sides, b=b: hip._launch(
+                                  "drift_gated_f32", *gated_side_args(gs[i % len(gs)], us[i % len(us)],
+                                                                      os_[i % len(os_)], b * 14336,
+                                                                      sides[i % len(sides)])), sets=n))
 
     # C3 prefill: per-head RMSNorm (eps 1e-6) + NeoX RoPE (theta 1e6)
     t, hq, hk, dim = 4096, 32, 8, 128
@@ -242,6 +288,15 @@ def cpu_baseline(kernels, budget_s: float):
         g, u = bits((units, 14336)), bits((units, 14336))
         return lambda: o.gated_bf16(0, g, u)
 
+    def rms_q8(units):
+        x = rng.standard_normal((units, 4096)).astype(np.float32)
+        return lambda: o.quantize_x(o.rms_norm(x, w4096, 1e-5))
+
+    def swiglu_q8(units):
+        g, u = rng.standard_normal((units, 14336)).astype(np.float32), rng.standard_normal((units, 14336)).astype(
+            np.float32)
+        return lambda: o.quantize_x(o.gated(0, g, u))
+
     def qk(units):
         q, k = bits((units, 32, 128)), bits((units, 8, 128))
         p = np.arange(units, dtype=np.int32)
@@ -272,6 +327,9 @@ def cpu_baseline(kernels, budget_s: float):
     for b in (1, 8, 64):
         work[f"rms_norm_bf16_b{b}"] = (rms, b, "rows")
         work[f"swiglu_bf16_b{b}"] = (swiglu, b, "rows")
+    for b in (1, 64):
+        work[f"rms_norm_q8_f32_b{b}"] = (rms_q8, b, "rows")
+        work[f"swiglu_q8_f32_b{b}"] = (swiglu_q8, b, "rows")
     work.update({"qk_norm_rope_bf16": (qk, 4096, "tokens"), "embedding_q8_0_bf16": (gather, 8192, "ids"),
                  "adaln_bf16": (adaln, 65520, "rows"), "gelu_tanh_bf16": (gelu, 65520, "rows"),
                  "rope_3d_bf16": (rope3d, 65520, "tokens")})
@@ -418,8 +476,9 @@ def main():
         "dtype": "bf16",
         "data": "synthetic (seeded device generators), resident in HBM; buffer sets rotated past the 256 MB MALL",
         "config": {
-            "workload": "drift fused layer kernels, one pass over C2 (decode B=1,8,64), C3 (prefill QK norm+RoPE), "
-                        "C4 (Q8_0 gather), C5 (Video DiT AdaLN, GELU-tanh, 3-D RoPE)",
+            "workload": "drift fused layer kernels, one pass over C2 (decode B=1,8,64; F32 with int8 side output "
+                        "B=1,64), C3 (prefill QK norm+RoPE), C4 (Q8_0 gather), C5 (Video DiT AdaLN, GELU-tanh, "
+                        "3-D RoPE)",
             "step_bytes": step_bytes,
             "parallelism": "single GPU",
         },

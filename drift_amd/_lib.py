@@ -26,16 +26,18 @@ SIGNATURES = {
     "drift_abi_version": (_I32, []),
     "drift_error_string": (ctypes.c_char_p, [_I32]),
     "drift_last_error": (ctypes.c_char_p, []),
-    "drift_rms_norm_f32": (_I32, [_P, _P, _P, _P, _I64, _I32, _F32, _F32, _I32, _P]),
-    "drift_rms_norm_bf16": (_I32, [_P, _P, _P, _P, _I64, _I32, _F32, _F32, _I32, _P]),
+    "drift_quantize_x_f32": (_I32, [_P, _P, _P, _P, _I64, _P]),
+    "drift_quantize_x_bf16": (_I32, [_P, _P, _P, _P, _I64, _P]),
+    "drift_rms_norm_f32": (_I32, [_P, _P, _P, _P, _I64, _I32, _F32, _F32, _I32, _P, _P, _P, _P]),
+    "drift_rms_norm_bf16": (_I32, [_P, _P, _P, _P, _I64, _I32, _F32, _F32, _I32, _P, _P, _P, _P]),
     "drift_layer_norm_f32": (_I32, [_P, _P, _P, _P, _I64, _I32, _F32, _P]),
     "drift_modulate_f32": (_I32, [_P, _P, _P, _P, _I64, _I32, _P]),
     "drift_layer_norm_modulate_f32": (_I32, [_P, _P, _P, _P, _I64, _I32, _I64, _F32, _P]),
     "drift_layer_norm_modulate_bf16": (_I32, [_P, _P, _P, _P, _I64, _I32, _I64, _F32, _P]),
     "drift_activation_f32": (_I32, [_P, _P, _I64, _I32, _F32, _P]),
     "drift_activation_bf16": (_I32, [_P, _P, _I64, _I32, _F32, _P]),
-    "drift_gated_f32": (_I32, [_P, _P, _P, _I64, _I32, _P]),
-    "drift_gated_bf16": (_I32, [_P, _P, _P, _I64, _I32, _P]),
+    "drift_gated_f32": (_I32, [_P, _P, _P, _I64, _I32, _P, _P, _P, _P]),
+    "drift_gated_bf16": (_I32, [_P, _P, _P, _I64, _I32, _P, _P, _P, _P]),
     "drift_rope_f32": (_I32, [_P, _P, _P, _I32, _I32, _I32, _I32, _F32, _I32, _I32, _I32, _I32, _I32, _I32, _P]),
     "drift_rope_bf16": (_I32, [_P, _P, _P, _I32, _I32, _I32, _I32, _F32, _I32, _I32, _I32, _I32, _I32, _I32, _P]),
     "drift_rope_table_f32": (_I32, [_P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _P]),
@@ -51,7 +53,7 @@ SIGNATURES = {
     "drift_convert": (_I32, [_P, _P, _I64, _I32, _P]),
 }
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 
 class NotBuilt(RuntimeError):

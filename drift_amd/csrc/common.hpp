@@ -125,7 +125,83 @@ __device__ __forceinline__ double group_sum(double v) {
   return v;
 }
 
+// ---------------------------------------------------------------- int8 side output
+
+// Where a kernel also writes its output quantized for the runner's int8
+// products (kernels/quantize.h:6-25): per block of 32 consecutive values of
+// the flat output, int8 codes xq[32 b + i], the scale xd[b] = max|v| / 127 and
+// xs[b] = xd[b] * sum of the codes. A null xq means no side output.
+struct Quantized {
+  int8_t* xq;
+  float* xd;
+  float* xs;
+};
+
+// A chunk's values as its store writes them: bf16 outputs rounded first, so
+// the codes describe what the output tensor holds.
+template <typename T, int N>
+__device__ __forceinline__ void as_written(float (&v)[N]) {
+  if constexpr (sizeof(T) == 2) {
+#pragma unroll
+    for (int j = 0; j < N; j += 2) {
+      const uint32_t pair = pack_bf16(v[j], v[j + 1]);
+      v[j] = bf16_lo(pair);
+      v[j + 1] = bf16_hi(pair);
+    }
+  }
+}
+
+// Quantizes a lane's N consecutive values, which with the other 32 / N - 1
+// lanes of its aligned lane group make up block `block`; every lane of the
+// group calls. The code is round-half-away(v / d) with d = max|v| / 127, both
+// divisions correctly rounded, and 0 where d is 0 or the quotient is NaN.
+template <int N>
+__device__ __forceinline__ void quantize_chunk(const float (&v)[N], int64_t block, Quantized q) {
+  constexpr int G = 32 / N;
+  float amax = fabsf(v[0]);
+#pragma unroll
+  for (int j = 1; j < N; ++j) amax = fmaxf(amax, fabsf(v[j]));
+#pragma unroll
+  for (int mask = 1; mask < G; mask <<= 1) amax = fmaxf(amax, __shfl_xor(amax, mask, G));
+  const float d = amax / 127.0f;
+  int sum = 0;
+  uint32_t bytes[(N + 3) / 4] = {};
+#pragma unroll
+  for (int j = 0; j < N; ++j) {
+    const float r = roundf(v[j] / d);
+    const int code = (d == 0.0f || r != r) ? 0 : (int)r;
+    sum += code;
+    bytes[j / 4] |= ((uint32_t)code & 0xffu) << (8 * (j % 4));
+  }
+  const int member = threadIdx.x % G;
+  int8_t* at = q.xq + block * 32 + member * N;
+  if constexpr (N == 1)
+    *at = (int8_t)bytes[0];
+  else if constexpr (N == 4)
+    *reinterpret_cast<uint32_t*>(at) = bytes[0];
+  else
+    *reinterpret_cast<uint2*>(at) = make_uint2(bytes[0], bytes[1]);
+#pragma unroll
+  for (int mask = 1; mask < G; mask <<= 1) sum += __shfl_xor(sum, mask, G);
+  if (member == 0) {
+    q.xd[block] = d;
+    q.xs[block] = d * (float)sum;
+  }
+}
+
 // ---------------------------------------------------------------- host side
+
+// quantize_x over `blocks` blocks of 32 values of x (quantize.hip): the side
+// output of a write that could not quantize as it wrote.
+int launch_quantize(const float* x, Quantized q, int64_t blocks, hipStream_t stream);
+int launch_quantize(const uint16_t* x, Quantized q, int64_t blocks, hipStream_t stream);
+// Whether a chunked kernel with N values per lane can store its codes (N
+// bytes per lane, 4- or 8-byte aligned stores).
+inline bool codes_storable(const int8_t* xq, int n) {
+  return (reinterpret_cast<uintptr_t>(xq) & (uintptr_t)(n >= 8 ? 7 : n >= 4 ? 3 : 0)) == 0;
+}
+// Checks a side output's pointers and block count; nonzero (refused) if bad.
+int check_quantized(const char* entry, Quantized q, int64_t values);
 
 // Records why an entry point refused its arguments (thread-local), returns
 // hipErrorInvalidValue.

@@ -167,8 +167,11 @@ __global__ void __launch_bounds__(256) activation_scalar(const T* x, T* out, int
     store_one(out + i, activate<kAccurate<T>>(kind, scale * load_one(x + i)));
 }
 
+// With q.xq, out is quantized too as it is written (quantize_chunk; n a
+// multiple of 32, so there is no tail and a wave's chunks are whole blocks).
 template <typename T, int KIND>
-__global__ void __launch_bounds__(256) gated_kernel(const T* gate, const T* up, T* out, int64_t n, int kind) {
+__global__ void __launch_bounds__(256) gated_kernel(const T* gate, const T* up, T* out, int64_t n, int kind,
+                                                    Quantized q) {
   constexpr int N = Chunk<T>::N;
   constexpr bool A = kAccurate<T>;
   const int k = KIND >= 0 ? KIND : kind;
@@ -182,6 +185,10 @@ __global__ void __launch_bounds__(256) gated_kernel(const T* gate, const T* up, 
 #pragma unroll
     for (int j = 0; j < N; ++j) g[j] = activate<A>(k, g[j]) * gated_up<A>(k, u[j]);
     Chunk<T>::store(out + i * N, g);
+    if (q.xq) {
+      as_written<T>(g);
+      quantize_chunk<N>(g, i * N / 32, q);
+    }
   }
   const int64_t tail = chunks * N + tid;
   if (tail < n) store_one(out + tail, activate<A>(k, load_one(gate + tail)) * gated_up<A>(k, load_one(up + tail)));
@@ -263,22 +270,34 @@ int activation(const char* entry, const T* x, T* out, int64_t n, int32_t kind, f
 }
 
 template <typename T>
-int gated(const char* entry, const T* gate, const T* up, T* out, int64_t n, int32_t kind, void* stream) {
+int gated(const char* entry, const T* gate, const T* up, T* out, int64_t n, int32_t kind, Quantized q,
+          void* stream) {
   clear_error();
   if (n < 0) return refuse("%s: %lld values", entry, (long long)n);
   if (kind < DRIFT_SILU || kind > DRIFT_SITU) return refuse("%s: no activation %d", entry, kind);
+  if (const int bad = check_quantized(entry, q, n)) return bad;
   if (n == 0) return 0;
   if (!gate || !up || !out) return refuse("%s: null gate, up or out", entry);
   const hipStream_t s = (hipStream_t)stream;
   constexpr int N = Chunk<T>::N;
-  if (aligned16(gate) && aligned16(up) && aligned16(out)) {
+  const bool chunked = aligned16(gate) && aligned16(up) && aligned16(out);
+  // the side output is written by the product when its chunks can store the
+  // codes, else by a quantize_x launch over out right after
+  const bool fused = q.xq && chunked && codes_storable(q.xq, N);
+  const Quantized in_kernel = fused ? q : Quantized{nullptr, nullptr, nullptr};
+  if (chunked) {
     const unsigned grid = grid_for(ceil_div(n, N), 256, 8192);
     if (kind == DRIFT_SILU)
-      hipLaunchKernelGGL((gated_kernel<T, DRIFT_SILU>), dim3(grid), dim3(256), 0, s, gate, up, out, n, kind);
+      hipLaunchKernelGGL((gated_kernel<T, DRIFT_SILU>), dim3(grid), dim3(256), 0, s, gate, up, out, n, kind,
+                         in_kernel);
     else
-      hipLaunchKernelGGL((gated_kernel<T, -1>), dim3(grid), dim3(256), 0, s, gate, up, out, n, kind);
+      hipLaunchKernelGGL((gated_kernel<T, -1>), dim3(grid), dim3(256), 0, s, gate, up, out, n, kind, in_kernel);
   } else {
     hipLaunchKernelGGL(gated_scalar<T>, dim3(grid_for(n, 256, 8192)), dim3(256), 0, s, gate, up, out, n, kind);
+  }
+  if (q.xq && !fused) {
+    if (const int status = launched(entry)) return status;
+    launch_quantize(out, q, n / 32, s);
   }
   return launched(entry);
 }
@@ -299,13 +318,13 @@ extern "C" int drift_activation_bf16(const uint16_t* x, uint16_t* out, int64_t n
 }
 
 extern "C" int drift_gated_f32(const float* gate, const float* up, float* out, int64_t n, int32_t kind,
-                               void* stream) {
-  return gated<float>("drift_gated_f32", gate, up, out, n, kind, stream);
+                               int8_t* xq, float* xd, float* xs, void* stream) {
+  return gated<float>("drift_gated_f32", gate, up, out, n, kind, Quantized{xq, xd, xs}, stream);
 }
 
 extern "C" int drift_gated_bf16(const uint16_t* gate, const uint16_t* up, uint16_t* out, int64_t n, int32_t kind,
-                                void* stream) {
-  return gated<uint16_t>("drift_gated_bf16", gate, up, out, n, kind, stream);
+                                int8_t* xq, float* xd, float* xs, void* stream) {
+  return gated<uint16_t>("drift_gated_bf16", gate, up, out, n, kind, Quantized{xq, xd, xs}, stream);
 }
 
 extern "C" int drift_convert(const void* x, void* out, int64_t n, int32_t kind, void* stream) {

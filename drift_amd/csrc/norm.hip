@@ -51,9 +51,12 @@ __device__ __forceinline__ void load_f32(const float* p, float (&v)[N]) {
 
 // ------------------------------------------------------------------ RMSNorm
 
+// With q.xq, out is quantized too as it is written (quantize_chunk; cols a
+// multiple of 32, so a row holds whole blocks).
 template <typename T, int K, int W>
 __global__ void __launch_bounds__(256) rms_norm_rows(T* x, const T* y, const float* weight, T* out, int64_t rows,
-                                                     int cols, float eps, float offset, int weight_rows) {
+                                                     int cols, float eps, float offset, int weight_rows,
+                                                     Quantized q) {
   constexpr int N = Chunk<T>::N;
   constexpr int kRowsPerBlock = 4 / W;
   __shared__ double partial[4];
@@ -93,6 +96,10 @@ __global__ void __launch_bounds__(256) rms_norm_rows(T* x, const T* y, const flo
 #pragma unroll
         for (int j = 0; j < N; ++j) o[j] = (float)((double)v[k][j] * factor * ((double)wv[j] + (double)offset));
         Chunk<T>::store(out + row * cols + c * N, o);
+        if (q.xq) {
+          as_written<T>(o);
+          quantize_chunk<N>(o, (row * cols + c * N) / 32, q);
+        }
       }
     }
   }
@@ -396,33 +403,43 @@ RowPlan plan_rows(int64_t rows, int cols, bool vector_ok) {
 
 template <typename T>
 int rms_norm(const char* entry, T* x, const T* y, const float* weight, T* out, int64_t rows, int32_t cols, float eps,
-             float offset, int32_t weight_rows, void* stream) {
+             float offset, int32_t weight_rows, Quantized q, void* stream) {
   clear_error();
   if (rows < 0) return refuse("%s: %lld rows", entry, (long long)rows);
   if (cols <= 0) return refuse("%s: rows of %d values", entry, cols);
   if (weight_rows <= 0) return refuse("%s: %d weight rows", entry, weight_rows);
+  if (q.xq && cols % 32 != 0) return refuse("%s: rows of %d values are not whole blocks of 32 to quantize", entry, cols);
+  if (const int bad = check_quantized(entry, q, rows * cols)) return bad;
   if (rows == 0) return 0;
   if (!x || !weight || !out) return refuse("%s: null x, weight or out", entry);
   const hipStream_t s = (hipStream_t)stream;
   const bool vector_ok = aligned16(x) && aligned16(out) && aligned16(weight) && (!y || aligned16(y));
   const RowPlan plan = plan_rows<T>(rows, cols, vector_ok);
+  // the side output is written by the norm when its chunks can store the
+  // codes, else by a quantize_x launch over out right after
+  const bool fused = q.xq && plan.per_lane > 0 && codes_storable(q.xq, Chunk<T>::N);
+  const Quantized in_kernel = fused ? q : Quantized{nullptr, nullptr, nullptr};
   if (plan.per_lane == 0) {
     hipLaunchKernelGGL(rms_norm_rows_scalar<T>, dim3(grid_for(rows, 1)), dim3(256), 0, s, x, y, weight, out, rows,
                        (int)cols, eps, offset, (int)weight_rows);
-    return launched(entry);
-  }
-  const unsigned grid = grid_for(rows, 4 / plan.waves);
-#define DRIFT_RMS_CASE(K)                                                                                       \
-  case K:                                                                                                       \
-    if (plan.waves == 1)                                                                                        \
-      hipLaunchKernelGGL((rms_norm_rows<T, K, 1>), dim3(grid), dim3(256), 0, s, x, y, weight, out, rows, cols, \
-                         eps, offset, weight_rows);                                                             \
-    else                                                                                                        \
-      hipLaunchKernelGGL((rms_norm_rows<T, K, 4>), dim3(grid), dim3(256), 0, s, x, y, weight, out, rows, cols, \
-                         eps, offset, weight_rows);                                                             \
+  } else {
+    const unsigned grid = grid_for(rows, 4 / plan.waves);
+#define DRIFT_RMS_CASE(K)                                                                                     \
+  case K:                                                                                                     \
+    if (plan.waves == 1)                                                                                      \
+      hipLaunchKernelGGL((rms_norm_rows<T, K, 1>), dim3(grid), dim3(256), 0, s, x, y, weight, out, rows,     \
+                         cols, eps, offset, weight_rows, in_kernel);                                          \
+    else                                                                                                      \
+      hipLaunchKernelGGL((rms_norm_rows<T, K, 4>), dim3(grid), dim3(256), 0, s, x, y, weight, out, rows,     \
+                         cols, eps, offset, weight_rows, in_kernel);                                          \
     break;
-  switch (plan.per_lane) { DRIFT_ROW_CASES(DRIFT_RMS_CASE) }
+    switch (plan.per_lane) { DRIFT_ROW_CASES(DRIFT_RMS_CASE) }
 #undef DRIFT_RMS_CASE
+  }
+  if (q.xq && !fused) {
+    if (const int status = launched(entry)) return status;
+    launch_quantize(out, q, rows * cols / 32, s);
+  }
   return launched(entry);
 }
 
@@ -506,14 +523,17 @@ int layer_norm(const char* entry, const T* x, const float* weight, const float* 
 using namespace drift;
 
 extern "C" int drift_rms_norm_f32(float* x, const float* y, const float* weight, float* out, int64_t rows,
-                                  int32_t cols, float eps, float offset, int32_t weight_rows, void* stream) {
-  return rms_norm<float>("drift_rms_norm_f32", x, y, weight, out, rows, cols, eps, offset, weight_rows, stream);
+                                  int32_t cols, float eps, float offset, int32_t weight_rows, int8_t* xq, float* xd,
+                                  float* xs, void* stream) {
+  return rms_norm<float>("drift_rms_norm_f32", x, y, weight, out, rows, cols, eps, offset, weight_rows,
+                         Quantized{xq, xd, xs}, stream);
 }
 
 extern "C" int drift_rms_norm_bf16(uint16_t* x, const uint16_t* y, const float* weight, uint16_t* out,
                                    int64_t rows, int32_t cols, float eps, float offset, int32_t weight_rows,
-                                   void* stream) {
-  return rms_norm<uint16_t>("drift_rms_norm_bf16", x, y, weight, out, rows, cols, eps, offset, weight_rows, stream);
+                                   int8_t* xq, float* xd, float* xs, void* stream) {
+  return rms_norm<uint16_t>("drift_rms_norm_bf16", x, y, weight, out, rows, cols, eps, offset, weight_rows,
+                            Quantized{xq, xd, xs}, stream);
 }
 
 extern "C" int drift_layer_norm_f32(const float* x, const float* weight, const float* bias, float* out,

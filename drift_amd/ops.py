@@ -20,8 +20,8 @@ from __future__ import annotations
 
 import ctypes
 import enum
-from dataclasses import dataclass
-from typing import Optional, Sequence
+from dataclasses import dataclass, replace
+from typing import Optional, Sequence, Tuple
 
 import torch
 
@@ -116,6 +116,34 @@ class Q8_0Table:
     @property
     def shape(self) -> tuple:
         return (self.data.shape[0], self.cols)
+
+
+@dataclass(frozen=True)
+class QuantizedValues:
+    """`values` F32 values at device address `address` that the launch
+    numbered `written` also wrote quantized into `buffer`: codes (int8 per
+    value), then scales, then code sums (F32 per block of 32)
+    (ops/HipBase.scala:129-147). Blocks do not depend on rows, so any whole
+    blocks within serve."""
+
+    address: int
+    values: int
+    buffer: torch.Tensor
+    written: int
+
+    def codes(self, first: int = 0, count: Optional[int] = None) -> torch.Tensor:
+        count = self.values - first if count is None else count
+        return self.buffer.narrow(0, first, count)
+
+    def scales(self, first: int = 0, count: Optional[int] = None) -> torch.Tensor:
+        blocks = self.values // 32
+        count = blocks - first if count is None else count
+        return self.buffer.narrow(0, self.values + 4 * first, 4 * count).view(torch.float32)
+
+    def sums(self, first: int = 0, count: Optional[int] = None) -> torch.Tensor:
+        blocks = self.values // 32
+        count = blocks - first if count is None else count
+        return self.buffer.narrow(0, self.values + 4 * blocks + 4 * first, 4 * count).view(torch.float32)
 
 
 # ------------------------------------------------------------------ checks
@@ -240,18 +268,99 @@ class HipOps:
 
     name = "hip"
 
+    # At most this many values are quantized as they are written: a decode
+    # step's inputs, not a prompt's (ops/HipBase.scala:150-154).
+    QuantizedMaximumValues = 8 * 16384
+
     def __init__(self, stream: Optional[torch.cuda.Stream] = None):
         _lib.load()
         self.stream = stream
         self.onWork = lambda: None  # ops/Ops.scala:29-33
+        # the int8 side output's bookkeeping (ops/HipBase.scala:117-214):
+        # launches so far, whether int8 products ran, what was last written
+        # quantized, and the buffers
+        self.deviceWrites = 0
+        self.quantizesX = False
+        self._quantizedValues: Optional[QuantizedValues] = None
+        self._quantizedBuffer: Optional[torch.Tensor] = None
+        self._scratch: Optional[torch.Tensor] = None
 
     def _stream(self):
         s = self.stream if self.stream is not None else torch.cuda.current_stream()
         return ctypes.c_void_p(s.cuda_stream)
 
     def _launch(self, entry: str, *args) -> None:
+        self.deviceWrites += 1
         self.onWork()
         _lib.call(entry, *args, self._stream())
+
+    def wrote(self) -> None:
+        """Counts a device write made outside these methods (a copy, a
+        torch op): what was written quantized before it no longer serves, as
+        every write the reference's backend makes counts
+        (ops/HipMemory.scala:57,97,141,147)."""
+        self.deviceWrites += 1
+
+    # ---------------------------------------------------------------- int8 side output
+
+    def quantizedTarget(self, out, cols: int) -> Tuple[Optional[QuantizedValues], tuple]:
+        """Where a kernel writing `out` (rows of `cols`) also writes it
+        quantized, when int8 products may read it, and the kernel's xq, xd,
+        xs pointers (nulls when not): ops/HipBase.scala:156-190."""
+        values = out.numel()
+        eligible = (self.quantizesX and out.dtype == F32 and values <= self.QuantizedMaximumValues
+                    and cols % 32 == 0)
+        if not eligible:
+            return None, (None, None, None)
+        size = values + 8 * (values // 32)
+        buffer = self._quantizedBuffer
+        if buffer is None or buffer.numel() < size or buffer.device != out.device:
+            buffer = torch.empty(max(size, 65536), dtype=torch.int8, device=out.device)
+            self._quantizedBuffer = buffer
+        target = QuantizedValues(out.data_ptr(), values, buffer, 0)
+        return target, (_ptr(target.codes()), _ptr(target.scales()), _ptr(target.sums()))
+
+    def wroteQuantized(self, target: Optional[QuantizedValues]) -> None:
+        """After the launch that wrote `target` (ops/HipBase.scala:191-193)."""
+        if target is not None:
+            self._quantizedValues = replace(target, written=self.deviceWrites)
+
+    def quantizedInput(self, x, m: int, k: int):
+        """`m` rows of `x` (`k` wide) as the last launch wrote them quantized,
+        if it did: (codes, scales, sums), ops/HipBase.scala:195-214."""
+        q = self._quantizedValues
+        if q is None or q.written != self.deviceWrites or x.dtype != F32:
+            return None
+        offset = x.data_ptr() - q.address
+        first = offset // 4
+        if offset >= 0 and offset % (4 * 32) == 0 and k % 32 == 0 and first + m * k <= q.values:
+            return q.codes(first, m * k), q.scales(first // 32, m * k // 32), q.sums(first // 32, m * k // 32)
+        return None
+
+    def quantize(self, x, m: int, k: int):
+        """`m` rows of `x` (`k` wide) quantized per 32 values into scratch
+        memory by quantize_x: (codes, scales, sums). Marks that int8 products
+        run, so the norms quantize as they write from now on
+        (ops/HipLinear.scala:366-386)."""
+        self.quantizesX = True
+        _require(x.dtype in (F32, BF16) and (m * k) % 32 == 0 and x.numel() >= m * k,
+                 f"quantize: {m} rows of {k} from {_shape(x)}")
+        _on_device("quantize", x)
+        blocks = m * k // 32
+        size = m * k + 8 * blocks
+        if self._scratch is None or self._scratch.numel() < size or self._scratch.device != x.device:
+            self._scratch = torch.empty(max(size, 65536), dtype=torch.int8, device=x.device)
+        q = QuantizedValues(0, m * k, self._scratch, 0)
+        codes, scales, sums = q.codes(), q.scales(), q.sums()
+        self._launch(f"drift_quantize_x_{_suffix(x.dtype)}", _ptr(x), _ptr(codes), _ptr(scales), _ptr(sums), blocks)
+        return codes, scales, sums
+
+    def productInput(self, x, m: int, k: int):
+        """What an int8 product over `m` rows of `x` reads: the side output
+        the launch that wrote x made, else x quantized now
+        (ops/HipLinear.scala:142-143)."""
+        found = self.quantizedInput(x, m, k)
+        return found if found is not None else self.quantize(x, m, k)
 
     # ---------------------------------------------------------------- norms
 
@@ -260,8 +369,18 @@ class HipOps:
         (ops/NormalisationOps.scala:30-45)."""
         rows = checkRowWise("rmsNorm", x, out, weight)
         _on_device("rmsNorm", x, weight, out)
-        self._launch(f"drift_rms_norm_{_suffix(x.dtype)}", _ptr(x), None, _ptr(weight), _ptr(out), rows,
-                     x.shape[-1], epsilon, weightOffset, 1)
+        self._normRows(x, None, weight, epsilon, weightOffset, out, rows)
+
+    def _normRows(self, x, y, weight, epsilon, weightOffset, out, rows) -> None:
+        """rms_norm over `rows`, `y` added to x first when given, out
+        quantized too when int8 products may read it
+        (ops/HipNormalisation.scala:83-115). Rows of 32 or fewer values take
+        the reference's narrow kernel there, which quantizes nothing."""
+        cols = x.shape[-1]
+        target, (xq, xd, xs) = self.quantizedTarget(out, cols) if cols > 32 else (None, (None, None, None))
+        self._launch(f"drift_rms_norm_{_suffix(x.dtype)}", _ptr(x), _ptr(y), _ptr(weight), _ptr(out), rows, cols,
+                     epsilon, weightOffset, 1, xq, xd, xs)
+        self.wroteQuantized(target)
 
     def addRmsNorm(self, x, y, norm: RowNorm) -> None:
         """`x += y`, then `norm`'s RMS norm of x into its out, in one launch
@@ -269,8 +388,7 @@ class HipOps:
         checkElementwise("addRmsNorm", x, y)
         rows = checkRowWise("addRmsNorm", x, norm.out, norm.weight)
         _on_device("addRmsNorm", x, y, norm.weight, norm.out)
-        self._launch(f"drift_rms_norm_{_suffix(x.dtype)}", _ptr(x), _ptr(y), _ptr(norm.weight), _ptr(norm.out),
-                     rows, x.shape[-1], norm.epsilon, norm.weightOffset, 1)
+        self._normRows(x, y, norm.weight, norm.epsilon, norm.weightOffset, norm.out, rows)
 
     def layerNorm(self, x, weight: Optional[torch.Tensor], bias: Optional[torch.Tensor], epsilon: float,
                   out) -> None:
@@ -322,7 +440,10 @@ class HipOps:
         """`out = kind(gate) * up` (ops/NormalisationOps.scala:21-24)."""
         checkElementwise("gated", gate, up, out)
         _on_device("gated", gate, up, out)
-        self._launch(f"drift_gated_{_suffix(gate.dtype)}", _ptr(gate), _ptr(up), _ptr(out), gate.numel(), int(kind))
+        target, (xq, xd, xs) = self.quantizedTarget(out, out.shape[-1])
+        self._launch(f"drift_gated_{_suffix(gate.dtype)}", _ptr(gate), _ptr(up), _ptr(out), gate.numel(), int(kind),
+                     xq, xd, xs)
+        self.wroteQuantized(target)
 
     # ---------------------------------------------------------------- rotary
 

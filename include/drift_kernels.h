@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define DRIFT_ABI_VERSION 1
+#define DRIFT_ABI_VERSION 2
 
 /* Activation kinds: src/drift/runner/ops/Activation.scala:6-20. */
 enum {
@@ -73,20 +73,39 @@ const char* drift_error_string(int code);
 /* Why the calling thread's last refused call was refused ("" if none). */
 const char* drift_last_error(void);
 
+/* ---------------------------------------------------------------- int8 side output
+ * The runner's int8 products read their input x quantized per block of 32
+ * consecutive values: codes xq[32 b + i] = round-half-away(x / xd[b]) (0 where
+ * xd[b] is 0), xd[b] = max |x| / 127 over the block, xs[b] = xd[b] * the sum
+ * of its codes (kernels/quantize.h:6-25). The norms and `gated` write it as
+ * they write `out` when given a non-null xq (then xd and xs non-null and
+ * 4-byte aligned, and the values whole blocks); for BF16 outputs it describes
+ * the rounded values out holds. It equals drift_quantize_x over `out`, bit for
+ * bit, as the reference's fused norms equal quantize_x
+ * (gpuTest/.../FusedOpsTests.scala:96-176).
+ *
+ * drift_quantize_x: `blocks` blocks of x quantized on their own. Replaces
+ * kernels/matvec.hip:392-397 quantize_x as launched by
+ * src/drift/runner/ops/HipLinear.scala:366-386. */
+int drift_quantize_x_f32(const float* x, int8_t* xq, float* xd, float* xs, int64_t blocks, void* stream);
+int drift_quantize_x_bf16(const uint16_t* x, int8_t* xq, float* xd, float* xs, int64_t blocks, void* stream);
+
 /* ---------------------------------------------------------------- RMSNorm
  * out = x / sqrt(mean(x^2) + eps) * (weight[r % weight_rows] + offset), per
  * row of `cols`. With `y` (nullable), x += y is written back first
- * (addRmsNorm). weight is F32 [weight_rows, cols].
- * Replaces kernels/norm.hip:34-41 rms_norm_f32 (int8 side outputs xq/xd/xs
- * not supported) as launched by src/drift/runner/ops/HipNormalisation.scala:57-131
- * (rmsNorm, normRows, addRmsNorm); the CPU definition is
- * ops/CpuNormalisation.scala:53-71. */
+ * (addRmsNorm). weight is F32 [weight_rows, cols]. With `xq` (nullable), the
+ * int8 side output of out, above (cols a multiple of 32).
+ * Replaces kernels/norm.hip:15-41 rms_norm_f32 as launched by
+ * src/drift/runner/ops/HipNormalisation.scala:57-131 (rmsNorm, normRows,
+ * addRmsNorm); the CPU definition is ops/CpuNormalisation.scala:53-71. */
 int drift_rms_norm_f32(float* x, const float* y, const float* weight, float* out, int64_t rows, int32_t cols,
-                       float eps, float offset, int32_t weight_rows, void* stream);
+                       float eps, float offset, int32_t weight_rows, int8_t* xq, float* xd, float* xs,
+                       void* stream);
 /* BF16 x, y, out; F32 weight. The reference's bf16 path is
  * convert -> rms_norm_f32 -> convert (kernels/elementwise.hip:68-86). */
 int drift_rms_norm_bf16(uint16_t* x, const uint16_t* y, const float* weight, uint16_t* out, int64_t rows,
-                        int32_t cols, float eps, float offset, int32_t weight_rows, void* stream);
+                        int32_t cols, float eps, float offset, int32_t weight_rows, int8_t* xq, float* xd, float* xs,
+                        void* stream);
 
 /* ---------------------------------------------------------------- LayerNorm, AdaLN
  * out = (x - mean) / sqrt(var + eps) * weight + bias; weight, bias nullable.
@@ -119,12 +138,14 @@ int drift_layer_norm_modulate_bf16(const uint16_t* x, const float* scale, const 
 int drift_activation_f32(const float* x, float* out, int64_t n, int32_t kind, float scale, void* stream);
 int drift_activation_bf16(const uint16_t* x, uint16_t* out, int64_t n, int32_t kind, float scale, void* stream);
 
-/* out = kind(gate) * up (SiTU soft-caps up as 25 tanh(up / 25)). Replaces
- * kernels/elementwise.hip:46-65 gated_f32 without its int8 side outputs
- * (ops/HipNormalisation.scala:32-47; CPU ops/CpuNormalisation.scala:22-41). */
-int drift_gated_f32(const float* gate, const float* up, float* out, int64_t n, int32_t kind, void* stream);
+/* out = kind(gate) * up (SiTU soft-caps up as 25 tanh(up / 25)); with `xq`
+ * (nullable), the int8 side output of out (n a multiple of 32). Replaces
+ * kernels/elementwise.hip:46-65 gated_f32 (ops/HipNormalisation.scala:32-47;
+ * CPU ops/CpuNormalisation.scala:22-41). */
+int drift_gated_f32(const float* gate, const float* up, float* out, int64_t n, int32_t kind, int8_t* xq,
+                    float* xd, float* xs, void* stream);
 int drift_gated_bf16(const uint16_t* gate, const uint16_t* up, uint16_t* out, int64_t n, int32_t kind,
-                     void* stream);
+                     int8_t* xq, float* xd, float* xs, void* stream);
 
 /* ---------------------------------------------------------------- RoPE
  * x, out [tokens, heads, head_dim]; positions int32 [positions_per_token,

@@ -380,3 +380,27 @@ int64_t oracle_embedding_f32(const float* table, int64_t vocab, int64_t cols, co
   }
   return -1;
 }
+
+/* kernels/quantize.h:10-25: a wave of 32 lanes holds a block, lane l its
+ * value l; amax is the fmaxf of |x| over the lanes, d = amax / 127.0f, the
+ * code int(roundf(x / d)) (0 for d == 0), its int8 kept; lane 0 writes d and
+ * d * float(sum of codes). fmaxf skips a NaN operand, so the order of the
+ * lanes' butterfly does not change amax. A NaN quotient (a NaN x, or an
+ * infinite d) gives code 0, as the GPU's float-to-int conversion does. */
+void oracle_quantize_x(const float* x, int8_t* xq, float* xd, float* xs, int64_t blocks) {
+  for (int64_t b = 0; b < blocks; ++b) {
+    const float* v = x + b * 32;
+    float amax = fabsf(v[0]);
+    for (int i = 1; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
+    const float d = amax / 127.0f;
+    int sum = 0;
+    for (int i = 0; i < 32; ++i) {
+      const float r = roundf(v[i] / d);
+      const int code = (d == 0.0f || r != r) ? 0 : (int)r;
+      xq[b * 32 + i] = (int8_t)code;
+      sum += code;
+    }
+    xd[b] = d;
+    xs[b] = d * (float)sum;
+  }
+}

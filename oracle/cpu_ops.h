@@ -81,6 +81,13 @@ int64_t oracle_embedding_q8_0(const uint8_t* table, int64_t vocab, int64_t cols,
 int64_t oracle_embedding_f32(const float* table, int64_t vocab, int64_t cols, const int32_t* ids, int64_t count,
                              float* out);
 
+/* ---- the int8 side output: kernels/quantize.h:10-25 (quantize_block),
+ *      kernels/matvec.hip:392-397 (quantize_x) ----
+ * Per block b of 32 consecutive values: xd[b] = max|x| / 127 (float
+ * division), xq[32 b + i] = (int8) roundf(x / xd[b]) (0 where xd[b] is 0 or
+ * the quotient is NaN), xs[b] = xd[b] * (float) sum of the block's codes. */
+void oracle_quantize_x(const float* x, int8_t* xq, float* xd, float* xs, int64_t blocks);
+
 #ifdef __cplusplus
 }
 #endif

@@ -78,6 +78,7 @@ def _declare(l: ctypes.CDLL) -> None:
         "oracle_wan_angles": (None, [_I32, _I32, _I32, _I32, _F64, _P, _P]),
         "oracle_embedding_q8_0": (_I64, [_P, _I64, _I64, _P, _I64, _P]),
         "oracle_embedding_f32": (_I64, [_P, _I64, _I64, _P, _I64, _P]),
+        "oracle_quantize_x": (None, [_P, _P, _P, _P, _I64]),
     }
     for name, (restype, argtypes) in sig.items():
         fn = getattr(l, name)
@@ -268,6 +269,20 @@ def embedding_f32(table, ids) -> np.ndarray:
     if bad >= 0:
         raise ValueError(f"token id {int(ids[bad])} outside the table")
     return out
+
+
+def quantize_x(x):
+    """The int8 side output of `x` (flat, whole blocks of 32): codes xq
+    (int8 [n]), scales xd and code sums xs (float32 [n / 32]),
+    kernels/quantize.h:10-25."""
+    x = _c(x, np.float32).ravel()
+    _need(x.size % 32 == 0, f"quantize_x: {x.size} values are not whole blocks of 32")
+    blocks = x.size // 32
+    xq = np.empty(x.size, np.int8)
+    xd = np.empty(blocks, np.float32)
+    xs = np.empty(blocks, np.float32)
+    lib().oracle_quantize_x(_ptr(x), _ptr(xq), _ptr(xd), _ptr(xs), blocks)
+    return xq, xd, xs
 
 
 # ---------------------------------------------------------------- bf16 compositions

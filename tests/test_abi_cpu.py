@@ -23,7 +23,7 @@ def test_header_and_library_agree(lib):
 
 
 def test_version_and_error_text(lib):
-    assert lib.drift_abi_version() == _lib.ABI_VERSION == 1
+    assert lib.drift_abi_version() == _lib.ABI_VERSION == 2
     assert lib.drift_error_string(0).decode().lower().startswith("no error")
     assert lib.drift_error_string(1)
 
@@ -38,21 +38,22 @@ def refused(lib, name, *args):
 
 def test_norms_refuse_bad_geometry(lib):
     p = ctypes.c_void_p(16)  # never dereferenced: validation fails first
-    assert "rows of 0 values" in refused(lib, "drift_rms_norm_f32", p, NULL, p, p, 4, 0, 1e-6, 0.0, 1, NULL)
-    assert "-1 rows" in refused(lib, "drift_rms_norm_bf16", p, NULL, p, p, -1, 8, 1e-6, 0.0, 1, NULL)
-    assert "weight rows" in refused(lib, "drift_rms_norm_f32", p, NULL, p, p, 4, 8, 1e-6, 0.0, 0, NULL)
-    assert "null" in refused(lib, "drift_rms_norm_f32", NULL, NULL, p, p, 4, 8, 1e-6, 0.0, 1, NULL)
+    no_q = (NULL, NULL, NULL)
+    assert "rows of 0 values" in refused(lib, "drift_rms_norm_f32", p, NULL, p, p, 4, 0, 1e-6, 0.0, 1, *no_q, NULL)
+    assert "-1 rows" in refused(lib, "drift_rms_norm_bf16", p, NULL, p, p, -1, 8, 1e-6, 0.0, 1, *no_q, NULL)
+    assert "weight rows" in refused(lib, "drift_rms_norm_f32", p, NULL, p, p, 4, 8, 1e-6, 0.0, 0, *no_q, NULL)
+    assert "null" in refused(lib, "drift_rms_norm_f32", NULL, NULL, p, p, 4, 8, 1e-6, 0.0, 1, *no_q, NULL)
     assert "rows per sample" in refused(lib, "drift_layer_norm_modulate_bf16", p, p, p, p, 4, 8, 0, 1e-6, NULL)
     assert "null scale or shift" in refused(lib, "drift_layer_norm_modulate_f32", p, NULL, p, p, 4, 8, 2, 1e-6, NULL)
     # empty input: success, nothing launched
-    assert lib.drift_rms_norm_f32(NULL, NULL, NULL, NULL, 0, 8, 1e-6, 0.0, 1, NULL) == 0
+    assert lib.drift_rms_norm_f32(NULL, NULL, NULL, NULL, 0, 8, 1e-6, 0.0, 1, *no_q, NULL) == 0
     assert lib.drift_layer_norm_f32(NULL, NULL, NULL, NULL, 0, 8, 1e-6, NULL) == 0
 
 
 def test_elementwise_refuses_bad_arguments(lib):
     p = ctypes.c_void_p(16)
     assert "no activation 5" in refused(lib, "drift_activation_f32", p, p, 10, 5, 1.0, NULL)
-    assert "no activation -1" in refused(lib, "drift_gated_bf16", p, p, p, 10, -1, NULL)
+    assert "no activation -1" in refused(lib, "drift_gated_bf16", p, p, p, 10, -1, NULL, NULL, NULL, NULL)
     assert "no conversion 7" in refused(lib, "drift_convert", p, ctypes.c_void_p(32), 10, 7, NULL)
     assert "same buffer" in refused(lib, "drift_convert", p, p, 10, 0, NULL)
     assert lib.drift_activation_bf16(NULL, NULL, 0, 1, 1.0, NULL) == 0
@@ -80,3 +81,16 @@ def test_embedding_refuses_partial_blocks(lib):
     assert "whole Q8_0 blocks" in refused(lib, "drift_embedding_q8_0_bf16", p, p, p, 4, 10, 48, NULL, NULL)
     assert "not 16-byte aligned" in refused(lib, "drift_embedding_q8_0_f32", p, p, ctypes.c_void_p(18), 4, 10, 64,
                                             NULL, NULL)
+
+
+def test_side_output_refuses_partial_blocks(lib):
+    p = ctypes.c_void_p(16)
+    q = (ctypes.c_void_p(64), ctypes.c_void_p(128), ctypes.c_void_p(256))
+    assert "whole blocks of 32" in refused(lib, "drift_rms_norm_f32", p, NULL, p, p, 4, 48, 1e-6, 0.0, 1, *q, NULL)
+    assert "whole blocks of 32" in refused(lib, "drift_gated_f32", p, p, p, 40, 0, *q, NULL)
+    assert "xd or xs" in refused(lib, "drift_gated_bf16", p, p, p, 64, 0, q[0], NULL, q[2], NULL)
+    assert "4-byte aligned" in refused(lib, "drift_rms_norm_bf16", p, NULL, p, p, 2, 64, 1e-6, 0.0, 1, q[0],
+                                       ctypes.c_void_p(130), q[2], NULL)
+    assert "null xq" in refused(lib, "drift_quantize_x_f32", p, NULL, q[1], q[2], 4, NULL)
+    assert "-2 blocks" in refused(lib, "drift_quantize_x_bf16", p, q[0], q[1], q[2], -2, NULL)
+    assert lib.drift_quantize_x_f32(NULL, NULL, NULL, NULL, 0, NULL) == 0
