@@ -7,7 +7,9 @@ A step is one pass of the path over its configurations, every kernel once:
   C3  prefill bf16: per-head RMSNorm + NeoX RoPE, Q [4096, 32, 128], K [4096, 8, 128]
   C4  Q8_0 gather of 8192 ids from [151936, 4096] to bf16
   C5  Video DiT block bf16: AdaLN [65520, 3072], GELU-tanh in place, 3-D RoPE
-      Q [65520, 24, 128] on the 21 x 30 x 52 grid
+      Q [65520, 24, 128] on the 21 x 30 x 52 grid; the gated residual with
+      per-sample gates, per-row modulation and gated residual from a
+      [65520, 6 x 3072] F32 table, and a per-head gate over [65520 x 24, 128]
 Inputs are synthetic (seeded device generators) and resident in HBM. Each
 kernel rotates through buffer sets totalling more than 512 MB, so the 256 MB
 Infinity Cache cannot hold what the next launch reads.
@@ -240,6 +242,32 @@ def make_kernels(hip: d.HipOps):
     nbytes = 2 * rows * 24 * 128 * 2
     kernels.append(Kernel("rope_3d_bf16", "C5 3-D RoPE bf16 Q[65520,24,128] grid 21x30x52 theta 1e4", nbytes, rows,
                           lambda i, n=n: hip.rope3d(qs5[i % n], 21, 30, 52, rq5[i % n]), sets=n))
+
+    # The same block's gated residuals and per-row modulation (bf16 x, F32
+    # gates and tables): x += gate[sample] * y; out = x * (1 + t[r][4]) +
+    # t[r][3] and x += t[r][5] * y over a [65520, 6 x 3072] table; and the
+    # per-head gate x[r] += g[r] * y[r] over [65520 x 24, 128]
+    ys5 = [randn_bf16((rows, width), 650 + i) for i in range(n)]
+    gates = (0.5 * torch.randn((2, width), generator=gen(8), device=DEV)).float()
+    nbytes = rows * width * 6 + 2 * width * 4
+    kernels.append(Kernel("gated_add_bf16", "C5 gated residual x += gate[sample] * y bf16 [65520,3072]", nbytes, rows,
+                          lambda i, n=n: hip.gatedAdd(xs5[i % n], ys5[i % n], gates, per), sets=n))
+    table = torch.empty((rows, 6 * width), dtype=torch.float32, device=DEV)
+    for lo in range(0, rows, 8192):
+        table[lo:lo + 8192] = 0.3 * torch.randn((min(8192, rows - lo), 6 * width), generator=gen(9), device=DEV)
+    nbytes = rows * width * (2 + 2 + 4 + 4)
+    kernels.append(Kernel("modulate_chunks_bf16", "C5 per-row modulation out = x*(1+t[r][4])+t[r][3] bf16 [65520,3072], "
+                          "t F32 [65520,18432]", nbytes, rows,
+                          lambda i, n=n: hip.modulateChunks(xs5[i % n], table, 3, 4, outs5[i % n]), sets=n))
+    nbytes = rows * width * (2 + 2 + 2 + 4)
+    kernels.append(Kernel("gated_add_chunk_bf16", "C5 per-row gated residual x += t[r][5] * y bf16 [65520,3072]",
+                          nbytes, rows, lambda i, n=n: hip.gatedAddChunk(xs5[i % n], ys5[i % n], table, 5), sets=n))
+    heads = rows * 24
+    head_gates = torch.rand(heads, generator=gen(10), device=DEV).float()
+    nbytes = heads * 128 * 6 + heads * 4
+    kernels.append(Kernel("row_gated_add_bf16", "per-head gate x[r] += g[r] * y[r] bf16 [65520*24,128]", nbytes, heads,
+                          lambda i, n=n: hip.rowGatedAdd(qs5[i % n].view(heads, 128), rq5[i % n].view(heads, 128),
+                                                         head_gates), sets=n))
     return kernels
 
 
@@ -314,6 +342,27 @@ def cpu_baseline(kernels, budget_s: float):
         x = bits((units, 3072))
         return lambda: o.activation_bf16(1, x)
 
+    g3072 = (0.5 * rng.standard_normal(3072)).astype(np.float32)
+
+    def gated_add(units):
+        x, y = o.from_bf16(bits((units, 3072))), o.from_bf16(bits((units, 3072)))
+        return lambda: o.to_bf16(o.gated_add(x, y, g3072))
+
+    def modulate_chunks(units):
+        x = o.from_bf16(bits((units, 3072)))
+        t = (0.3 * rng.standard_normal((units, 6 * 3072))).astype(np.float32)
+        return lambda: o.to_bf16(o.modulate_chunks(x, t, 3, 4))
+
+    def gated_add_chunk(units):
+        x, y = o.from_bf16(bits((units, 3072))), o.from_bf16(bits((units, 3072)))
+        t = (0.3 * rng.standard_normal((units, 6 * 3072))).astype(np.float32)
+        return lambda: o.to_bf16(o.gated_add_chunk(x, y, t, 5))
+
+    def row_gated_add(units):
+        x, y = o.from_bf16(bits((units, 128))), o.from_bf16(bits((units, 128)))
+        g = rng.random(units).astype(np.float32)
+        return lambda: o.to_bf16(o.row_gated_add(x, y, g))
+
     cos, sin = o.wan_angles(21, 30, 52)  # Wan keeps a grid's tables (models/Wan.scala:324-330)
 
     def rope3d(units):
@@ -332,7 +381,10 @@ def cpu_baseline(kernels, budget_s: float):
         work[f"swiglu_q8_f32_b{b}"] = (swiglu_q8, b, "rows")
     work.update({"qk_norm_rope_bf16": (qk, 4096, "tokens"), "embedding_q8_0_bf16": (gather, 8192, "ids"),
                  "adaln_bf16": (adaln, 65520, "rows"), "gelu_tanh_bf16": (gelu, 65520, "rows"),
-                 "rope_3d_bf16": (rope3d, 65520, "tokens")})
+                 "rope_3d_bf16": (rope3d, 65520, "tokens"), "gated_add_bf16": (gated_add, 65520, "rows"),
+                 "modulate_chunks_bf16": (modulate_chunks, 65520, "rows"),
+                 "gated_add_chunk_bf16": (gated_add_chunk, 65520, "rows"),
+                 "row_gated_add_bf16": (row_gated_add, 65520 * 24, "head rows")})
     # Each kernel gets 2/3 of budget_s / 11 seconds on one core: a sample of
     # up to the whole launch's units, run once untimed and then again until
     # that time is spent; the per-run time is what scales to the whole
@@ -478,7 +530,7 @@ def main():
         "config": {
             "workload": "drift fused layer kernels, one pass over C2 (decode B=1,8,64; F32 with int8 side output "
                         "B=1,64), C3 (prefill QK norm+RoPE), C4 (Q8_0 gather), C5 (Video DiT AdaLN, GELU-tanh, "
-                        "3-D RoPE)",
+                        "3-D RoPE, gated residuals, per-row modulation)",
             "step_bytes": step_bytes,
             "parallelism": "single GPU",
         },

@@ -34,6 +34,14 @@ SIGNATURES = {
     "drift_modulate_f32": (_I32, [_P, _P, _P, _P, _I64, _I32, _P]),
     "drift_layer_norm_modulate_f32": (_I32, [_P, _P, _P, _P, _I64, _I32, _I64, _F32, _P]),
     "drift_layer_norm_modulate_bf16": (_I32, [_P, _P, _P, _P, _I64, _I32, _I64, _F32, _P]),
+    "drift_gated_add_f32": (_I32, [_P, _P, _P, _I64, _I32, _I64, _P]),
+    "drift_gated_add_bf16": (_I32, [_P, _P, _P, _I64, _I32, _I64, _P]),
+    "drift_modulate_chunks_f32": (_I32, [_P, _P, _P, _I64, _I32, _I32, _I32, _I32, _P]),
+    "drift_modulate_chunks_bf16": (_I32, [_P, _P, _P, _I64, _I32, _I32, _I32, _I32, _P]),
+    "drift_gated_add_chunk_f32": (_I32, [_P, _P, _P, _I64, _I32, _I32, _I32, _P]),
+    "drift_gated_add_chunk_bf16": (_I32, [_P, _P, _P, _I64, _I32, _I32, _I32, _P]),
+    "drift_row_gated_add_f32": (_I32, [_P, _P, _P, _I64, _I32, _P]),
+    "drift_row_gated_add_bf16": (_I32, [_P, _P, _P, _I64, _I32, _P]),
     "drift_activation_f32": (_I32, [_P, _P, _I64, _I32, _F32, _P]),
     "drift_activation_bf16": (_I32, [_P, _P, _I64, _I32, _F32, _P]),
     "drift_gated_f32": (_I32, [_P, _P, _P, _I64, _I32, _P, _P, _P, _P]),

@@ -20,7 +20,7 @@ constexpr int kWave = 64;
 __device__ __forceinline__ float bf16_lo(uint32_t pair) { return __uint_as_float(pair << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t pair) { return __uint_as_float(pair & 0xffff0000u); }
 
-// Float to BF16 bits as CpuOps.toBfloat16 rounds (ops/CpuOps.scala:426-431):
+// Float to BF16 bits as CpuOps.toBfloat16 rounds (ops/CpuOps.scala:52-57):
 // nearest even on the bit pattern; a NaN keeps its top half, quiet bit set.
 // gfx950's v_cvt_pk_bf16_f32 does exactly this, two values per instruction
 // (checked on the device over every class of pattern, NaN payloads and ties

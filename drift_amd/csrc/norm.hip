@@ -8,7 +8,7 @@
 // instruction of a wave covers 1 KiB of contiguous memory.
 //
 // Arithmetic is the runner's CPU reference's (ops/CpuNormalisation.scala:53-71,
-// :128-151, ops/CpuElementwise.scala:212-217): sums, factor and every output in
+// :128-151, ops/CpuElementwise.scala:33-38): sums, factor and every output in
 // double, rounded once to float (then to bf16). CDNA4 runs double at the same
 // vector rate as unpacked float, so this costs no more than float math and
 // the results match the reference to the last bit but for sums taken in

@@ -191,6 +191,30 @@ def checkRowWise(operation: str, x, out, *rowVectors) -> int:
     return x.numel() // x.shape[-1] if x.shape[-1] else 0
 
 
+def checkChunks(operation: str, x, table, out, *indices) -> tuple:
+    """Returns (rows, C, chunks): x, out [rows, C], table F32
+    [rows, chunks * C], every index a chunk (ops/ElementwiseOps.scala:55-76)."""
+    checkElementwise(operation, x, out)
+    requireF32(operation, table)
+    _require(x.dim() == 2, f"{operation} takes [rows, C], not {_shape(x)}")
+    rows, channels = x.shape
+    width = table.shape[-1] if table.dim() else 0
+    _require(table.dim() == 2 and table.shape[0] == rows and channels > 0 and width % channels == 0
+             and all(0 <= i < width // channels for i in indices),
+             f"{operation}: table {_shape(table)} for {_shape(x)}, chunks ArraySeq({', '.join(map(str, indices))})")
+    return rows, channels, width // channels
+
+
+def checkRowGatedAdd(x, y, gate) -> tuple:
+    """Returns (rows, cols) (ops/ElementwiseOps.scala:79-92)."""
+    checkElementwise("rowGatedAdd", x, y)
+    requireF32("rowGatedAdd", gate)
+    _require(x.dim() == 2, f"rowGatedAdd takes [rows, cols], not {_shape(x)}")
+    rows, cols = x.shape
+    _require(gate.numel() == rows, f"rowGatedAdd: gate {_shape(gate)} for {_shape(x)}")
+    return rows, cols
+
+
 def checkRope(x, positions, rope: Rope, out) -> tuple:
     """ops/AttentionOps.scala:185-223; returns (tokens, heads, headDimension)."""
     checkElementwise("rope", x, out)
@@ -384,7 +408,7 @@ class HipOps:
 
     def addRmsNorm(self, x, y, norm: RowNorm) -> None:
         """`x += y`, then `norm`'s RMS norm of x into its out, in one launch
-        (ops/NormalisationOps.scala:131-138, ops/HipNormalisation.scala:117-131)."""
+        (ops/NormalisationOps.scala:42-45, ops/HipNormalisation.scala:117-131)."""
         checkElementwise("addRmsNorm", x, y)
         rows = checkRowWise("addRmsNorm", x, norm.out, norm.weight)
         _on_device("addRmsNorm", x, y, norm.weight, norm.out)
@@ -405,6 +429,52 @@ class HipOps:
         requireF32("modulate", x)
         _on_device("modulate", x, scale, shift, out)
         self._launch("drift_modulate_f32", _ptr(x), _ptr(scale), _ptr(shift), _ptr(out), rows, x.shape[-1])
+
+    # ---------------------------------------------------------------- gated residuals
+
+    def gatedAdd(self, x, y, gate, rowsPerSample: Optional[int] = None) -> None:
+        """`x += gate * y` in place (ops/ElementwiseOps.scala:30-31). `gate` is
+        F32 [cols], one vector for every row, as the reference's; or, beyond
+        it, [samples, cols] with sample s's row for rows
+        [s * rowsPerSample, (s + 1) * rowsPerSample)."""
+        if gate.dim() <= 1:
+            rows = checkRowWise("gatedAdd", x, y, gate)
+            per = max(rows, 1)
+        else:
+            checkElementwise("gatedAdd", x, y)
+            requireF32("gatedAdd", gate)
+            cols = x.shape[-1]
+            rows = x.numel() // cols if cols else 0
+            _require(rowsPerSample is not None and rowsPerSample > 0, "gatedAdd: per-sample gates need rowsPerSample")
+            samples = -(-rows // rowsPerSample)
+            _require(gate.dim() == 2 and tuple(gate.shape) == (samples, cols),
+                     f"gatedAdd: {_shape(gate)} for {samples} samples of rows of {cols}")
+            per = rowsPerSample
+        _on_device("gatedAdd", x, y, gate)
+        self._launch(f"drift_gated_add_{_suffix(x.dtype)}", _ptr(x), _ptr(y), _ptr(gate), rows, x.shape[-1], per)
+
+    def modulateChunks(self, x, table, shift: int, scale: int, out) -> None:
+        """`out = x * (1 + table chunk scale) + table chunk shift`, x, out
+        [rows, C], table F32 [rows, chunks * C] (ops/ElementwiseOps.scala:33-43)."""
+        rows, channels, chunks = checkChunks("modulateChunks", x, table, out, shift, scale)
+        _on_device("modulateChunks", x, table, out)
+        self._launch(f"drift_modulate_chunks_{_suffix(x.dtype)}", _ptr(x), _ptr(table), _ptr(out), rows, channels,
+                     chunks, shift, scale)
+
+    def gatedAddChunk(self, x, y, table, gate: int) -> None:
+        """`x += table chunk gate * y`, the tables as modulateChunks'
+        (ops/ElementwiseOps.scala:45-46)."""
+        rows, channels, chunks = checkChunks("gatedAddChunk", x, table, y, gate)
+        _on_device("gatedAddChunk", x, y, table)
+        self._launch(f"drift_gated_add_chunk_{_suffix(x.dtype)}", _ptr(x), _ptr(y), _ptr(table), rows, channels,
+                     chunks, gate)
+
+    def rowGatedAdd(self, x, y, gate) -> None:
+        """`x[r] += gate[r] * y[r]`: one gate per row, gate F32 [rows]
+        (ops/ElementwiseOps.scala:48-49)."""
+        rows, cols = checkRowGatedAdd(x, y, gate)
+        _on_device("rowGatedAdd", x, y, gate)
+        self._launch(f"drift_row_gated_add_{_suffix(x.dtype)}", _ptr(x), _ptr(y), _ptr(gate), rows, cols)
 
     def layerNormModulate(self, x, scale, shift, epsilon: float, out, rowsPerSample: Optional[int] = None) -> None:
         """AdaLN in one launch: layerNorm(x, None, None, epsilon) then

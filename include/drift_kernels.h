@@ -14,7 +14,7 @@
  * Element types: F32 is float; BF16 is uint16_t holding the top half of an
  * F32, rounded to nearest even from float results (NaN keeps its top half with
  * the quiet bit set), as the runner's CpuOps.toBfloat16
- * (runner/src/drift/runner/ops/CpuOps.scala:426-431). Norm, modulation and
+ * (runner/src/drift/runner/ops/CpuOps.scala:52-57). Norm, modulation and
  * rope vectors are F32; positions and ids are int32.
  *
  * Arithmetic follows the runner's CPU reference (`CpuOps`): statistics,
@@ -115,7 +115,7 @@ int drift_layer_norm_f32(const float* x, const float* weight, const float* bias,
                          int32_t cols, float eps, void* stream);
 
 /* out = x * (1 + scale[c]) + shift[c]. Replaces kernels/elementwise.hip:97-103
- * modulate_f32 (ops/HipElementwise.scala:77-89; CPU ops/CpuElementwise.scala:212-217). */
+ * modulate_f32 (ops/HipElementwise.scala:77-89; CPU ops/CpuElementwise.scala:33-38). */
 int drift_modulate_f32(const float* x, const float* scale, const float* shift, float* out, int64_t rows,
                        int32_t cols, void* stream);
 
@@ -130,6 +130,42 @@ int drift_layer_norm_modulate_f32(const float* x, const float* scale, const floa
 int drift_layer_norm_modulate_bf16(const uint16_t* x, const float* scale, const float* shift, uint16_t* out,
                                    int64_t rows, int32_t cols, int64_t rows_per_sample, float eps,
                                    void* stream);
+
+/* ---------------------------------------------------------------- gated residuals
+ * The steps either side of a diffusion block's modulated norms, in place on
+ * x [rows, cols] (F32, or BF16 with F32 gates and tables); every value is
+ * computed in double and rounded once, as the CPU reference does
+ * (ops/CpuElementwise.scala:40-86).
+ *
+ * x[r][c] += gate[r / rows_per_sample][c] * y[r][c], gate F32
+ * [ceil(rows / rows_per_sample), cols]; rows_per_sample = rows is the
+ * reference's one gate vector. Replaces kernels/elementwise.hip:105-108
+ * gated_add_f32 (ops/HipElementwise.scala:91-102). */
+int drift_gated_add_f32(float* x, const float* y, const float* gate, int64_t rows, int32_t cols,
+                        int64_t rows_per_sample, void* stream);
+int drift_gated_add_bf16(uint16_t* x, const uint16_t* y, const float* gate, int64_t rows, int32_t cols,
+                         int64_t rows_per_sample, void* stream);
+/* out[r][c] = x[r][c] * (1 + table[r][scale][c]) + table[r][shift][c], table
+ * F32 [rows, chunks * channels]; out may be x. Replaces
+ * kernels/elementwise.hip:110-121 modulate_chunks_f32
+ * (ops/HipElementwise.scala:104-126). */
+int drift_modulate_chunks_f32(const float* x, const float* table, float* out, int64_t rows, int32_t channels,
+                              int32_t chunks, int32_t shift, int32_t scale, void* stream);
+int drift_modulate_chunks_bf16(const uint16_t* x, const float* table, uint16_t* out, int64_t rows, int32_t channels,
+                               int32_t chunks, int32_t shift, int32_t scale, void* stream);
+/* x[r][c] += table[r][gate][c] * y[r][c], the tables as modulate_chunks'.
+ * Replaces kernels/elementwise.hip:123-130 gated_add_chunk_f32
+ * (ops/HipElementwise.scala:128-143). */
+int drift_gated_add_chunk_f32(float* x, const float* y, const float* table, int64_t rows, int32_t channels,
+                              int32_t chunks, int32_t gate, void* stream);
+int drift_gated_add_chunk_bf16(uint16_t* x, const uint16_t* y, const float* table, int64_t rows, int32_t channels,
+                               int32_t chunks, int32_t gate, void* stream);
+/* x[r][c] += gate[r] * y[r][c], gate F32 [rows]. Replaces
+ * kernels/elementwise.hip:132-138 row_gated_add_f32
+ * (ops/HipElementwise.scala:145-157). */
+int drift_row_gated_add_f32(float* x, const float* y, const float* gate, int64_t rows, int32_t cols, void* stream);
+int drift_row_gated_add_bf16(uint16_t* x, const uint16_t* y, const float* gate, int64_t rows, int32_t cols,
+                             void* stream);
 
 /* ---------------------------------------------------------------- activations
  * out = kind(scale * x), elementwise over n values. Replaces

@@ -21,7 +21,7 @@ static float bits_float(uint32_t b) {
   return v;
 }
 
-/* CpuOps.toBfloat16 (ops/CpuOps.scala:426-431): round to nearest even on the
+/* CpuOps.toBfloat16 (ops/CpuOps.scala:52-57): round to nearest even on the
  * bit pattern; a NaN keeps its top half with the quiet bit set. */
 uint16_t oracle_to_bf16(float value) {
   const uint32_t bits = float_bits(value);
@@ -33,7 +33,7 @@ uint16_t oracle_to_bf16(float value) {
 float oracle_from_bf16(uint16_t bits) { return bits_float((uint32_t)bits << 16); }
 
 /* Float.float16ToFloat as LittleEndian.float16 uses it
- * (tensor/LittleEndian.scala:147-148): exact, subnormals included; a NaN keeps
+ * (tensor/LittleEndian.scala:45-46): exact, subnormals included; a NaN keeps
  * its significand shifted into the float's top bits. */
 float oracle_f16_to_f32(uint16_t h) {
   const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
@@ -95,7 +95,7 @@ void oracle_f16_to_f32_n(const uint16_t* x, float* out, int64_t n) {
   for (int64_t i = 0; i < n; ++i) out[i] = oracle_f16_to_f32(x[i]);
 }
 
-/* CpuOps.erf (ops/CpuOps.scala:400-424): odd; the Maclaurin series of erf
+/* CpuOps.erf (ops/CpuOps.scala:26-50): odd; the Maclaurin series of erf
  * below 2.5, summed until a term no longer moves the sum; the continued
  * fraction of erfc, 60 levels deep, from 2.5 on. */
 double oracle_erf(double x) {
@@ -148,8 +148,8 @@ void oracle_gated(int kind, const float* gate, const float* up, float* out, int6
     out[i] = (float)(oracle_activate(kind, (double)gate[i]) * gated_up(kind, (double)up[i]));
 }
 
-/* Ops.addRmsNorm's two steps (ops/NormalisationOps.scala:135-138): add
- * (ops/CpuElementwise.scala:188-192), then CpuNormalisation.rmsNorm
+/* Ops.addRmsNorm's two steps (ops/NormalisationOps.scala:42-45): add
+ * (ops/CpuElementwise.scala:9-13), then CpuNormalisation.rmsNorm
  * (ops/CpuNormalisation.scala:53-71): the squares summed in double, the factor
  * 1/sqrt(mean + eps) in double, each value x * factor * (w + offset) in
  * double, rounded to float. */
@@ -193,7 +193,7 @@ void oracle_layer_norm(const float* x, const float* weight, const float* bias, f
   }
 }
 
-/* CpuElementwise.modulate (ops/CpuElementwise.scala:212-217) */
+/* CpuElementwise.modulate (ops/CpuElementwise.scala:33-38) */
 void oracle_modulate(const float* x, const float* scale, const float* shift, float* out, int64_t rows,
                      int64_t cols) {
   for (int64_t r = 0; r < rows; ++r)
@@ -204,7 +204,7 @@ void oracle_modulate(const float* x, const float* scale, const float* shift, flo
 }
 
 /* The section a pair takes its position from (ops/CpuAttention.scala:98-108,
- * ops/Rope.scala:245-268). */
+ * ops/Rope.scala:12-35). */
 static int rope_section(int pair, int sections, const int32_t* s) {
   switch (sections) {
     case 1:
@@ -403,4 +403,55 @@ void oracle_quantize_x(const float* x, int8_t* xq, float* xd, float* xs, int64_t
     xd[b] = d;
     xs[b] = d * (float)sum;
   }
+}
+
+/* ops/CpuElementwise.scala:40-49 gatedAdd: before(i) + gates(i % cols) *
+ * added(i), in double (the reader widens every float), written as float. A
+ * batch of samples takes sample r / rows_per_sample's gate row. */
+void oracle_gated_add(float* x, const float* y, const float* gate, int64_t rows, int64_t cols,
+                      int64_t rows_per_sample) {
+  for (int64_t r = 0; r < rows; ++r) {
+    const float* g = gate + (r / rows_per_sample) * cols;
+    for (int64_t c = 0; c < cols; ++c) {
+      const int64_t i = r * cols + c;
+      x[i] = (float)((double)x[i] + (double)g[c] * (double)y[i]);
+    }
+  }
+}
+
+/* ops/CpuElementwise.scala:51-67 modulateChunks: input(index) * (1 +
+ * values(row + scale * channels + c)) + values(row + shift * channels + c),
+ * row = r * chunks * channels, in double. */
+void oracle_modulate_chunks(const float* x, const float* table, float* out, int64_t rows, int64_t channels,
+                            int64_t chunks, int64_t shift, int64_t scale) {
+  for (int64_t r = 0; r < rows; ++r) {
+    const float* row = table + r * chunks * channels;
+    for (int64_t c = 0; c < channels; ++c) {
+      const int64_t i = r * channels + c;
+      out[i] = (float)((double)x[i] * (1.0 + (double)row[scale * channels + c]) + (double)row[shift * channels + c]);
+    }
+  }
+}
+
+/* ops/CpuElementwise.scala:69-79 gatedAddChunk: input(index) +
+ * values(r * chunks * channels + gate * channels + c) * other(index). */
+void oracle_gated_add_chunk(float* x, const float* y, const float* table, int64_t rows, int64_t channels,
+                            int64_t chunks, int64_t gate) {
+  for (int64_t r = 0; r < rows; ++r) {
+    const float* g = table + r * chunks * channels + gate * channels;
+    for (int64_t c = 0; c < channels; ++c) {
+      const int64_t i = r * channels + c;
+      x[i] = (float)((double)x[i] + (double)g[c] * (double)y[i]);
+    }
+  }
+}
+
+/* ops/CpuElementwise.scala:81-85 rowGatedAdd: input(index) + gates(index /
+ * cols) * other(index). */
+void oracle_row_gated_add(float* x, const float* y, const float* gate, int64_t rows, int64_t cols) {
+  for (int64_t r = 0; r < rows; ++r)
+    for (int64_t c = 0; c < cols; ++c) {
+      const int64_t i = r * cols + c;
+      x[i] = (float)((double)x[i] + (double)gate[r] * (double)y[i]);
+    }
 }

@@ -21,8 +21,8 @@
 extern "C" {
 #endif
 
-/* ---- conversions: ops/CpuOps.scala:426-431, tensor/DType.scala:99-102,
- *      tensor/LittleEndian.scala:147-148 ---- */
+/* ---- conversions: ops/CpuOps.scala:52-57, tensor/DType.scala:99-102,
+ *      tensor/LittleEndian.scala:45-46 ---- */
 uint16_t oracle_to_bf16(float value);
 float oracle_from_bf16(uint16_t bits);
 float oracle_f16_to_f32(uint16_t bits);
@@ -32,7 +32,7 @@ void oracle_bf16_to_f32_n(const uint16_t* x, float* out, int64_t n);
 void oracle_f32_to_f16_n(const float* x, uint16_t* out, int64_t n);
 void oracle_f16_to_f32_n(const uint16_t* x, float* out, int64_t n);
 
-/* ---- ops/CpuOps.scala:400-424 ---- */
+/* ---- ops/CpuOps.scala:26-50 ---- */
 double oracle_erf(double x);
 
 /* ---- ops/CpuNormalisation.scala:11-41 (kinds: ops/Activation.scala:6-20) ---- */
@@ -40,8 +40,8 @@ double oracle_activate(int kind, double v);
 void oracle_activation(int kind, float input_scale, const float* x, float* out, int64_t n);
 void oracle_gated(int kind, const float* gate, const float* up, float* out, int64_t n);
 
-/* ---- ops/CpuElementwise.scala:188-192 (add), ops/CpuNormalisation.scala:53-71
- *      (rmsNorm), ops/NormalisationOps.scala:135-138 (addRmsNorm) ----
+/* ---- ops/CpuElementwise.scala:9-13 (add), ops/CpuNormalisation.scala:53-71
+ *      (rmsNorm), ops/NormalisationOps.scala:42-45 (addRmsNorm) ----
  * With `y`, x += y first (written back), then the norm of x into out. Row r
  * uses weight row r % weight_rows. */
 void oracle_rms_norm(float* x, const float* y, const float* weight, float* out, int64_t rows, int64_t cols,
@@ -51,7 +51,7 @@ void oracle_rms_norm(float* x, const float* y, const float* weight, float* out, 
 void oracle_layer_norm(const float* x, const float* weight, const float* bias, float* out, int64_t rows,
                        int64_t cols, float eps);
 
-/* ---- ops/CpuElementwise.scala:212-217 ---- */
+/* ---- ops/CpuElementwise.scala:33-38 ---- */
 void oracle_modulate(const float* x, const float* scale, const float* shift, float* out, int64_t rows,
                      int64_t cols);
 
@@ -80,6 +80,19 @@ int64_t oracle_embedding_q8_0(const uint8_t* table, int64_t vocab, int64_t cols,
 /* ---- F32 tables: ops/CpuLinear.scala:12-41 with DType.F32 ---- */
 int64_t oracle_embedding_f32(const float* table, int64_t vocab, int64_t cols, const int32_t* ids, int64_t count,
                              float* out);
+
+/* ---- gated residuals and per-row modulation: ops/CpuElementwise.scala:40-86 ----
+ * In place on x [rows, cols] (gatedAdd, gatedAddChunk, rowGatedAdd) or into
+ * out (modulateChunks); tables are [rows, chunks * cols]. gatedAdd's gate is
+ * [ceil(rows / rows_per_sample), cols] (rows_per_sample = rows: the
+ * reference's one vector). */
+void oracle_gated_add(float* x, const float* y, const float* gate, int64_t rows, int64_t cols,
+                      int64_t rows_per_sample);
+void oracle_modulate_chunks(const float* x, const float* table, float* out, int64_t rows, int64_t channels,
+                            int64_t chunks, int64_t shift, int64_t scale);
+void oracle_gated_add_chunk(float* x, const float* y, const float* table, int64_t rows, int64_t channels,
+                            int64_t chunks, int64_t gate);
+void oracle_row_gated_add(float* x, const float* y, const float* gate, int64_t rows, int64_t cols);
 
 /* ---- the int8 side output: kernels/quantize.h:10-25 (quantize_block),
  *      kernels/matvec.hip:392-397 (quantize_x) ----

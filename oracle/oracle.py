@@ -79,6 +79,10 @@ def _declare(l: ctypes.CDLL) -> None:
         "oracle_embedding_q8_0": (_I64, [_P, _I64, _I64, _P, _I64, _P]),
         "oracle_embedding_f32": (_I64, [_P, _I64, _I64, _P, _I64, _P]),
         "oracle_quantize_x": (None, [_P, _P, _P, _P, _I64]),
+        "oracle_gated_add": (None, [_P, _P, _P, _I64, _I64, _I64]),
+        "oracle_modulate_chunks": (None, [_P, _P, _P, _I64, _I64, _I64, _I64, _I64]),
+        "oracle_gated_add_chunk": (None, [_P, _P, _P, _I64, _I64, _I64, _I64]),
+        "oracle_row_gated_add": (None, [_P, _P, _P, _I64, _I64]),
     }
     for name, (restype, argtypes) in sig.items():
         fn = getattr(l, name)
@@ -103,7 +107,7 @@ def _c(a, dtype) -> np.ndarray:
 # ---------------------------------------------------------------- conversions
 
 def to_bf16(x) -> np.ndarray:
-    """F32 -> BF16 bits, CpuOps.toBfloat16 (ops/CpuOps.scala:426-431)."""
+    """F32 -> BF16 bits, CpuOps.toBfloat16 (ops/CpuOps.scala:52-57)."""
     x = _c(x, np.float32)
     out = np.empty(x.shape, np.uint16)
     lib().oracle_f32_to_bf16_n(_ptr(x), _ptr(out), x.size)
@@ -126,7 +130,7 @@ def to_f16(x) -> np.ndarray:
 
 
 def from_f16(bits) -> np.ndarray:
-    """F16 bits -> F32, Float.float16ToFloat (tensor/LittleEndian.scala:147-148)."""
+    """F16 bits -> F32, Float.float16ToFloat (tensor/LittleEndian.scala:45-46)."""
     bits = _c(bits, np.uint16)
     out = np.empty(bits.shape, np.float32)
     lib().oracle_f16_to_f32_n(_ptr(bits), _ptr(out), bits.size)
@@ -268,6 +272,57 @@ def embedding_f32(table, ids) -> np.ndarray:
     bad = lib().oracle_embedding_f32(_ptr(table), vocab, cols, _ptr(ids), ids.size, _ptr(out))
     if bad >= 0:
         raise ValueError(f"token id {int(ids[bad])} outside the table")
+    return out
+
+
+def gated_add(x, y, gate, rows_per_sample=None) -> np.ndarray:
+    """x + gate * y per row (ops/CpuElementwise.scala:40-49), returned (x is
+    not changed). gate [cols], or [samples, cols] with rows_per_sample."""
+    out = np.array(x, dtype=np.float32, copy=True, order="C")
+    y, gate = _c(y, np.float32), _c(gate, np.float32)
+    _need(y.shape == out.shape and out.ndim >= 1, f"gated_add: x {out.shape}, y {y.shape}")
+    cols = out.shape[-1]
+    rows = out.size // cols
+    per = rows if rows_per_sample is None else rows_per_sample
+    _need(per > 0 and gate.size == -(-rows // per) * cols, f"gated_add: gate {gate.shape} for {out.shape}")
+    lib().oracle_gated_add(_ptr(out), _ptr(y), _ptr(gate), rows, cols, per)
+    return out
+
+
+def _chunks(x, table, *indices):
+    _need(x.ndim == 2 and table.ndim == 2 and table.shape[0] == x.shape[0] and table.shape[1] % x.shape[1] == 0,
+          f"table {table.shape} for {x.shape}")
+    chunks = table.shape[1] // x.shape[1]
+    _need(all(0 <= i < chunks for i in indices), f"chunks {indices} of {chunks}")
+    return x.shape[0], x.shape[1], chunks
+
+
+def modulate_chunks(x, table, shift: int, scale: int) -> np.ndarray:
+    """ops/CpuElementwise.scala:51-67."""
+    x, table = _c(x, np.float32), _c(table, np.float32)
+    rows, channels, chunks = _chunks(x, table, shift, scale)
+    out = np.empty_like(x)
+    lib().oracle_modulate_chunks(_ptr(x), _ptr(table), _ptr(out), rows, channels, chunks, shift, scale)
+    return out
+
+
+def gated_add_chunk(x, y, table, gate: int) -> np.ndarray:
+    """ops/CpuElementwise.scala:69-79, returned."""
+    out = np.array(x, dtype=np.float32, copy=True, order="C")
+    y, table = _c(y, np.float32), _c(table, np.float32)
+    _need(y.shape == out.shape, f"gated_add_chunk: x {out.shape}, y {y.shape}")
+    rows, channels, chunks = _chunks(out, table, gate)
+    lib().oracle_gated_add_chunk(_ptr(out), _ptr(y), _ptr(table), rows, channels, chunks, gate)
+    return out
+
+
+def row_gated_add(x, y, gate) -> np.ndarray:
+    """ops/CpuElementwise.scala:81-85, returned."""
+    out = np.array(x, dtype=np.float32, copy=True, order="C")
+    y, gate = _c(y, np.float32), _c(gate, np.float32)
+    _need(y.shape == out.shape and out.ndim == 2 and gate.size == out.shape[0],
+          f"row_gated_add: x {out.shape}, y {y.shape}, gate {gate.shape}")
+    lib().oracle_row_gated_add(_ptr(out), _ptr(y), _ptr(gate), out.shape[0], out.shape[1])
     return out
 
 

@@ -94,3 +94,15 @@ def test_side_output_refuses_partial_blocks(lib):
     assert "null xq" in refused(lib, "drift_quantize_x_f32", p, NULL, q[1], q[2], 4, NULL)
     assert "-2 blocks" in refused(lib, "drift_quantize_x_bf16", p, q[0], q[1], q[2], -2, NULL)
     assert lib.drift_quantize_x_f32(NULL, NULL, NULL, NULL, 0, NULL) == 0
+
+
+def test_gated_residuals_refuse_bad_geometry(lib):
+    p = ctypes.c_void_p(16)
+    assert "rows per sample" in refused(lib, "drift_gated_add_f32", p, p, p, 4, 8, 0, NULL)
+    assert "rows of 0 values" in refused(lib, "drift_gated_add_bf16", p, p, p, 4, 0, 4, NULL)
+    assert "chunk 6 of 6" in refused(lib, "drift_modulate_chunks_f32", p, p, p, 4, 8, 6, 0, 6, NULL)
+    assert "chunk -1 of 6" in refused(lib, "drift_gated_add_chunk_bf16", p, p, p, 4, 8, 6, -1, NULL)
+    assert "0 chunks per row" in refused(lib, "drift_modulate_chunks_bf16", p, p, p, 4, 8, 0, 0, 0, NULL)
+    assert "-3 rows" in refused(lib, "drift_row_gated_add_f32", p, p, p, -3, 8, NULL)
+    assert "null operand" in refused(lib, "drift_row_gated_add_bf16", p, NULL, p, 3, 8, NULL)
+    assert lib.drift_gated_add_f32(NULL, NULL, NULL, 0, 8, 1, NULL) == 0

@@ -79,3 +79,30 @@ def test_convert_rules(hip):
 def test_host_tensors_are_refused_before_launch(hip):
     with pytest.raises(ValueError, match="device memory"):
         hip.rmsNorm(f32(2, 4), f32(4), 1e-6, 0.0, f32(2, 4))
+
+
+def test_gated_residual_rules(hip):
+    # ops/ElementwiseOps.scala:55-92, ops/Ops.scala:76-92
+    with pytest.raises(ValueError, match=r"gatedAdd: \[3\] for rows of 4"):
+        hip.gatedAdd(f32(2, 4), f32(2, 4), f32(3))
+    with pytest.raises(ValueError, match="equal shapes"):
+        hip.gatedAdd(f32(2, 4), f32(3, 4), f32(4))
+    with pytest.raises(ValueError, match="rowsPerSample"):
+        hip.gatedAdd(f32(4, 4), f32(4, 4), f32(2, 4))
+    with pytest.raises(ValueError, match=r"gatedAdd: \[3, 4\] for 2 samples"):
+        hip.gatedAdd(f32(4, 4), f32(4, 4), f32(3, 4), rowsPerSample=2)
+    with pytest.raises(ValueError, match=r"modulateChunks takes \[rows, C\], not \[2, 2, 4\]"):
+        hip.modulateChunks(f32(2, 2, 4), f32(2, 24), 0, 1, f32(2, 2, 4))
+    with pytest.raises(ValueError, match=r"modulateChunks: table \[2, 10\] for \[2, 4\], chunks ArraySeq\(0, 1\)"):
+        hip.modulateChunks(f32(2, 4), f32(2, 10), 0, 1, f32(2, 4))
+    with pytest.raises(ValueError, match=r"gatedAddChunk: table \[2, 24\] for \[2, 4\], chunks ArraySeq\(6\)"):
+        hip.gatedAddChunk(f32(2, 4), f32(2, 4), f32(2, 24), 6)
+    with pytest.raises(ValueError, match="takes F32, not BF16"):
+        hip.gatedAddChunk(f32(2, 4), f32(2, 4), bf16(2, 24), 2)
+    with pytest.raises(ValueError, match=r"rowGatedAdd takes \[rows, cols\], not \[8\]"):
+        hip.rowGatedAdd(f32(8), f32(8), f32(1))
+    with pytest.raises(ValueError, match=r"rowGatedAdd: gate \[3\] for \[2, 4\]"):
+        hip.rowGatedAdd(f32(2, 4), f32(2, 4), f32(3))
+    # a call that passes the rules stops at the device check
+    with pytest.raises(ValueError, match="device memory"):
+        hip.gatedAddChunk(f32(2, 4), f32(2, 4), f32(2, 24), 5)

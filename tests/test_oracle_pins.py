@@ -157,7 +157,7 @@ def test_erf_against_abramowitz_stegun():
 
 
 def test_erf_against_libm():
-    # the reference documents its erf as good to about 1e-15 (ops/CpuOps.scala:400-402);
+    # the reference documents its erf as good to about 1e-15 (ops/CpuOps.scala:26-28);
     # its series gives up a few more ulps just below 2.5
     for x in np.linspace(-6, 6, 1201):
         assert abs(o.erf(float(x)) - math.erf(float(x))) < 1e-14
