@@ -1,6 +1,7 @@
 // Elementwise kernels for gfx950: activations, gated activations (SwiGLU and
-// kin) and float-type conversions. Each thread streams 16-byte chunks
-// (8 bf16 or 4 F32 values) with a grid-stride loop, two chunks in flight.
+// kin) and float-type conversions. A thread takes one 16-byte chunk (8 bf16
+// or 4 F32 values) and the grid covers the tensor in one pass (a grid-stride
+// loop only past 2^30 blocks).
 //
 // The runner's CPU reference computes activations in double
 // (ops/CpuNormalisation.scala:11-24). Here they run in float through forms
@@ -120,30 +121,7 @@ __global__ void __launch_bounds__(256) activation_kernel(const T* x, T* out, int
   const int64_t chunks = n / N;
   const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  int64_t i = tid;
-  for (; i + stride < chunks; i += 2 * stride) {
-    float a[N], b[N];
-    Chunk<T>::load(x + i * N, a);
-    Chunk<T>::load(x + (i + stride) * N, b);
-    if constexpr (KIND == DRIFT_GELU_TANH && !A) {
-#pragma unroll
-      for (int j = 0; j < N; ++j) {
-        a[j] *= scale;
-        b[j] *= scale;
-      }
-      gelu_tanh_fast(a);
-      gelu_tanh_fast(b);
-    } else {
-#pragma unroll
-      for (int j = 0; j < N; ++j) {
-        a[j] = activate<A>(k, scale * a[j]);
-        b[j] = activate<A>(k, scale * b[j]);
-      }
-    }
-    Chunk<T>::store(out + i * N, a);
-    Chunk<T>::store(out + (i + stride) * N, b);
-  }
-  if (i < chunks) {
+  for (int64_t i = tid; i < chunks; i += stride) {
     float a[N];
     Chunk<T>::load(x + i * N, a);
     if constexpr (KIND == DRIFT_GELU_TANH && !A) {
@@ -250,7 +228,7 @@ int activation(const char* entry, const T* x, T* out, int64_t n, int32_t kind, f
   const hipStream_t s = (hipStream_t)stream;
   constexpr int N = Chunk<T>::N;
   if (aligned16(x) && aligned16(out)) {
-    const unsigned grid = grid_for(ceil_div(n, 2 * N), 256, 8192);
+    const unsigned grid = grid_for(ceil_div(n, N), 256, kOneShotBlocks);
     switch (kind) {
       case DRIFT_SILU:
         hipLaunchKernelGGL((activation_kernel<T, DRIFT_SILU>), dim3(grid), dim3(256), 0, s, x, out, n, kind, scale);
@@ -286,7 +264,7 @@ int gated(const char* entry, const T* gate, const T* up, T* out, int64_t n, int3
   const bool fused = q.xq && chunked && codes_storable(q.xq, N);
   const Quantized in_kernel = fused ? q : Quantized{nullptr, nullptr, nullptr};
   if (chunked) {
-    const unsigned grid = grid_for(ceil_div(n, N), 256, 8192);
+    const unsigned grid = grid_for(ceil_div(n, N), 256, kOneShotBlocks);
     if (kind == DRIFT_SILU)
       hipLaunchKernelGGL((gated_kernel<T, DRIFT_SILU>), dim3(grid), dim3(256), 0, s, gate, up, out, n, kind,
                          in_kernel);

@@ -14,9 +14,9 @@
 // the reference's double sum does; the modulation rounds 1 + s, the product
 // and the sum in double in the reference's order (-ffp-contract=off).
 //
-// Layout: x, y, out row-major [rows, cols] of T; a lane takes 16-byte chunks
-// (4 F32 or 8 BF16) of the flat tensor, grid-stride, two at a time with
-// every load issued first. A chunk's row comes from a double multiply by
+// Layout: x, y, out row-major [rows, cols] of T; a lane takes one 16-byte
+// chunk (4 F32 or 8 BF16) of the flat tensor and the grid covers it in one
+// pass. A chunk's row comes from a double multiply by
 // 1 / chunks-per-row, corrected by one step, rather than a 64-bit division.
 #include "common.hpp"
 
@@ -48,15 +48,17 @@ __device__ __forceinline__ int64_t quotient(int64_t i, int64_t d, double inverse
   return q;
 }
 
-template <int N>
+// N consecutive F32 factors. A row's table chunk is read once (streamed); a
+// sample's gate row is read by every row of the sample (cached).
+template <int N, bool STREAM>
 __device__ __forceinline__ void load_floats(const float* p, float (&v)[N]) {
 #pragma unroll
   for (int j = 0; j < N; j += 4) {
-    const float4 q = *reinterpret_cast<const float4*>(p + j);
-    v[j] = q.x;
-    v[j + 1] = q.y;
-    v[j + 2] = q.z;
-    v[j + 3] = q.w;
+    const uint4 q = STREAM ? stream_load(p + j) : *reinterpret_cast<const uint4*>(p + j);
+    v[j] = __uint_as_float(q.x);
+    v[j + 1] = __uint_as_float(q.y);
+    v[j + 2] = __uint_as_float(q.z);
+    v[j + 3] = __uint_as_float(q.w);
   }
 }
 
@@ -73,7 +75,7 @@ struct Operands {
     x = Chunk<T>::load_raw(xs + i * N);
     if constexpr (OP != MODULATE_CHUNKS) y = Chunk<T>::load_raw(ys + i * N);
     if constexpr (OP == GATED_ADD) {
-      load_floats<N>(v + quotient(r, m.per, m.per_inverse) * m.cols + c, a);
+      load_floats<N, false>(v + quotient(r, m.per, m.per_inverse) * m.cols + c, a);
     } else if constexpr (OP == ROW_GATED_ADD) {
       const float g = v[r];
 #pragma unroll
@@ -81,10 +83,10 @@ struct Operands {
     } else {
       const float* row = v + r * m.chunks * (int64_t)m.cols + c;
       if constexpr (OP == GATED_ADD_CHUNK) {
-        load_floats<N>(row + (int64_t)m.first * m.cols, a);
+        load_floats<N, true>(row + (int64_t)m.first * m.cols, a);
       } else {
-        load_floats<N>(row + (int64_t)m.second * m.cols, a);
-        load_floats<N>(row + (int64_t)m.first * m.cols, b);
+        load_floats<N, true>(row + (int64_t)m.second * m.cols, a);
+        load_floats<N, true>(row + (int64_t)m.first * m.cols, b);
       }
     }
   }
@@ -109,15 +111,7 @@ template <typename T, int OP>
 __global__ void __launch_bounds__(256) row_map_chunks(const T* x, const T* y, const float* v, T* out, RowMap m,
                                                       int64_t total) {
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  for (; i + stride < total; i += 2 * stride) {
-    Operands<T, OP> p, q;
-    p.load(x, y, v, m, i);
-    q.load(x, y, v, m, i + stride);
-    p.apply(out, i);
-    q.apply(out, i + stride);
-  }
-  if (i < total) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
     Operands<T, OP> p;
     p.load(x, y, v, m, i);
     p.apply(out, i);
@@ -167,8 +161,8 @@ int row_map(const char* entry, const T* x, const T* y, const float* v, T* out, R
     m.row_chunks = m.cols / N;
     m.row_inverse = 1.0 / (double)m.row_chunks;
     const int64_t total = values / N;
-    hipLaunchKernelGGL((row_map_chunks<T, OP>), dim3(grid_for(ceil_div(total, 2), 256, 8192)), dim3(256), 0, s, x,
-                       y, v, out, m, total);
+    hipLaunchKernelGGL((row_map_chunks<T, OP>), dim3(grid_for(total, 256, kOneShotBlocks)), dim3(256), 0, s, x, y,
+                       v, out, m, total);
   } else {
     hipLaunchKernelGGL((row_map_values<T, OP>), dim3(grid_for(values, 256, 8192)), dim3(256), 0, s, x, y, v, out, m,
                        values, 1.0 / (double)m.cols);
