@@ -105,13 +105,31 @@ __device__ __forceinline__ void store_one(uint16_t* p, float v) { *p = (uint16_t
 
 // ---------------------------------------------------------------- reductions
 
+// A double moved across lanes by a DPP pattern (both halves), within rows of
+// 16 lanes.
+template <int kCtrl>
+__device__ __forceinline__ double dpp_move(double v) {
+  const uint64_t bits = __builtin_bit_cast(uint64_t, v);
+  const int lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)bits, kCtrl, 0xf, 0xf, true);
+  const int hi = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)(bits >> 32), kCtrl, 0xf, 0xf, true);
+  return __builtin_bit_cast(double, ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
+}
+
 // Sum over aligned groups of `width` lanes (a power of two up to 64); every
-// lane of a group gets the group's total. The butterfly order is fixed, so a
-// row's sum does not depend on how many rows share the launch.
+// lane of a group gets the group's total. It is the xor butterfly (partners
+// i ^ 1, i ^ 2, ...), its steps inside 16-lane rows taken by DPP moves: after
+// the first two, the lanes of a quad hold one value, so the half-row and row
+// mirrors (i <-> 7 - i, i <-> 15 - i) add the same partners as i ^ 4 and
+// i ^ 8. The order is fixed, so a row's sum does not depend on how many rows
+// share the launch.
 template <int width>
 __device__ __forceinline__ double group_sum(double v) {
+  if constexpr (width > 1) v += dpp_move<0xb1>(v);   // quad_perm [1, 0, 3, 2]
+  if constexpr (width > 2) v += dpp_move<0x4e>(v);   // quad_perm [2, 3, 0, 1]
+  if constexpr (width > 4) v += dpp_move<0x141>(v);  // row_half_mirror
+  if constexpr (width > 8) v += dpp_move<0x140>(v);  // row_mirror
 #pragma unroll
-  for (int mask = 1; mask < width; mask <<= 1) v += __shfl_xor(v, mask, width);
+  for (int mask = 16; mask < width; mask <<= 1) v += __shfl_xor(v, mask, width);
   return v;
 }
 

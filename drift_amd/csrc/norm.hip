@@ -16,6 +16,8 @@
 #include "common.hpp"
 
 #include <algorithm>
+#include <atomic>
+#include <climits>
 
 namespace drift {
 namespace {
@@ -249,60 +251,141 @@ __global__ void __launch_bounds__(256) layer_norm_rows_scalar(const T* x, const 
   }
 }
 
-// AdaLN over one sample's rows, one wave per row: the sample's (1 + scale,
-// shift) are made once per block, in double, into LDS laid out
-// [value of chunk][chunk], so the 64 lanes of a wave reading value j of their
-// chunks read 64 consecutive 16-byte entries (no bank conflicts). Blocks are
-// persistent over their sample's rows (grid.y = sample), so the table costs
-// one pass per block, not per row.
+// F32 AdaLN, one wave per row, four rows of one sample per block (grid.y =
+// sample), the grid covering the rows in one pass. Each lane reads its
+// chunks' scale and shift from the sample's rows (cached: every row of the
+// sample reads them).
 //
-// The mean and variance come from one pass over the row in double about its
-// first value x0 (sums of d = x - x0 and d^2): the same as the reference's two
+// The mean and variance come from one pass over the row about its first
+// value x0 (sums of d = x - x0 and d^2): the same as the reference's two
 // passes to the last bits, since |mean - x0| is a few standard deviations at
-// most. n = float((x - mean) * factor) is the reference layerNorm's F32
-// result; out = n * (1 + scale) + shift in double, rounded once, as modulate.
+// most. The arithmetic is the reference's, in double: n = float((x - mean) *
+// factor) is layerNorm's F32 result, out = n * (1 + scale) + shift rounded
+// once, as modulate.
+constexpr int kAdalnMaxCols = 4096;
+
 template <typename T, int K, bool FULL>
-__global__ void __launch_bounds__(512) adaln_rows(const T* x, const float* scale, const float* shift, T* out,
-                                                  int64_t rows, int cols, int64_t rows_per_sample, float eps) {
+__global__ void __launch_bounds__(256) adaln_waves(const T* x, const float* scale, const float* shift, T* out,
+                                                    int64_t rows, int cols, int64_t rows_per_sample, float eps) {
   constexpr int N = Chunk<T>::N;
   using Raw = typename Chunk<T>::Raw;
-  extern __shared__ double2 table[];  // [N][chunks]
-  // with whole rows of K wave-chunks the table's stride is a constant, so
-  // every LDS read takes its offset as an immediate
   const int chunks = FULL ? K * kWave : cols / N;
   const int64_t sample = blockIdx.y;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t row = sample * rows_per_sample + (int64_t)blockIdx.x * 4 + wave;
+  if (row >= min(rows, (sample + 1) * rows_per_sample)) return;
+  Raw raw[K];
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int c = k * kWave + lane;
+    if (FULL || c < chunks) raw[k] = Chunk<T>::load_raw(x + row * cols + c * N);
+  }
+  float first_value[N];
+  Chunk<T>::unpack(raw[0], first_value);
+  const double x0 = (double)__shfl(first_value[0], 0);
+  double s1 = 0.0, s2 = 0.0;
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    if (FULL || k * kWave + lane < chunks) {
+      float v[N];
+      Chunk<T>::unpack(raw[k], v);
+#pragma unroll
+      for (int j = 0; j < N; ++j) {
+        const double d = (double)v[j] - x0;
+        s1 += d;
+        s2 = fma(d, d, s2);
+      }
+    }
+  }
+  s1 = group_sum<64>(s1);
+  s2 = group_sum<64>(s2);
+  const double m1 = s1 / (double)cols;  // mean - x0
+  const double mean = x0 + m1;
+  const double variance = fmax(s2 / (double)cols - m1 * m1, 0.0);
+  const double factor = 1.0 / sqrt(variance + (double)eps);
+  const double offset = -mean * factor;
   const float* sc = scale + sample * cols;
   const float* sh = shift + sample * cols;
-  for (int c = threadIdx.x; c < cols; c += blockDim.x)
-    table[(c % N) * chunks + c / N] = make_double2(1.0 + (double)sc[c], (double)sh[c]);
-  __syncthreads();
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
-  const int64_t first = sample * rows_per_sample;
-  const int64_t end = min(rows, first + rows_per_sample);
-  const int64_t stride = (int64_t)gridDim.x * waves;
-  int64_t row = first + (int64_t)blockIdx.x * waves + wave;
-  Raw raw[K];
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int c = k * kWave + lane;
+    if (FULL || c < chunks) {
+      float v[N], o[N], a[N], b[N];
+      Chunk<T>::unpack(raw[k], v);
+      load_f32<N>(sc + c * N, a);
+      load_f32<N>(sh + c * N, b);
+#pragma unroll
+      for (int j = 0; j < N; ++j) {
+        const float n = (float)fma((double)v[j], factor, offset);
+        o[j] = (float)fma((double)n, 1.0 + (double)a[j], (double)b[j]);
+      }
+      Chunk<T>::store(out + row * cols + c * N, o);
+    }
+  }
+}
+
+// BF16 AdaLN with each lane's (1 + scale, shift) held in registers across the
+// rows it takes: re-reading them per row would move four times the row's own
+// bytes through the L1. Wave w of a sample takes rows w, w + W, w + 2W, ... of
+// it (W waves per sample, all resident at once), with the next row's loads in
+// flight while it computes the current one.
+//
+// The arithmetic is adaln_waves', in double. It has to be: where the output
+// nearly cancels (n * (1 + scale) ~ -shift) a float ulp of n or of 1 + scale
+// is many bf16 ulps of the result. d = x - x0 is exact in float for bf16
+// values within a factor 2^15 of each other, and d^2 exact in double.
+template <int K, bool FULL>
+__global__ void __launch_bounds__(256) adaln_resident(const uint16_t* x, const float* scale, const float* shift,
+                                                      uint16_t* out, int64_t rows, int cols, int64_t rows_per_sample,
+                                                      float eps, int64_t waves_per_sample) {
+  constexpr int N = 8;
+  using Raw = uint4;
+  const int chunks = FULL ? K * kWave : cols / N;
+  const int64_t sample = blockIdx.y;
+  const int lane = threadIdx.x & 63;
+  const int64_t w = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t end = min(rows, (sample + 1) * rows_per_sample);
+  int64_t row = sample * rows_per_sample + w;
+  if (w >= waves_per_sample || row >= end) return;
   auto load_row = [&](int64_t r, Raw(&into)[K]) {
 #pragma unroll
     for (int k = 0; k < K; ++k) {
       const int c = k * kWave + lane;
-      if (FULL || c < chunks) into[k] = Chunk<T>::load_raw(x + r * cols + c * N);
+      if (FULL || c < chunks) into[k] = Chunk<uint16_t>::load_raw(x + r * cols + c * N);
     }
   };
-  if (row < end) load_row(row, raw);
-  for (; row < end; row += stride) {
+  Raw raw[K];
+  load_row(row, raw);
+  double a[K][N];
+  float b[K][N];
+  const float* sc = scale + sample * cols;
+  const float* sh = shift + sample * cols;
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int c = k * kWave + lane;
+    if (FULL || c < chunks) {
+      float f[N];
+      load_f32<N>(sc + c * N, f);
+      load_f32<N>(sh + c * N, b[k]);
+#pragma unroll
+      for (int j = 0; j < N; ++j) a[k][j] = 1.0 + (double)f[j];
+    }
+  }
+  for (; row < end; row += waves_per_sample) {
+    Raw next[K];
+    if (row + waves_per_sample < end) load_row(row + waves_per_sample, next);
     float first_value[N];
-    Chunk<T>::unpack(raw[0], first_value);
-    const double x0 = (double)__shfl(first_value[0], 0);
+    Chunk<uint16_t>::unpack(raw[0], first_value);
+    const float x0 = __shfl(first_value[0], 0);
     double s1 = 0.0, s2 = 0.0;
 #pragma unroll
     for (int k = 0; k < K; ++k) {
       if (FULL || k * kWave + lane < chunks) {
         float v[N];
-        Chunk<T>::unpack(raw[k], v);
+        Chunk<uint16_t>::unpack(raw[k], v);
 #pragma unroll
         for (int j = 0; j < N; ++j) {
-          const double d = (double)v[j] - x0;
+          const double d = (double)(v[j] - x0);
           s1 += d;
           s2 = fma(d, d, s2);
         }
@@ -311,7 +394,7 @@ __global__ void __launch_bounds__(512) adaln_rows(const T* x, const float* scale
     s1 = group_sum<64>(s1);
     s2 = group_sum<64>(s2);
     const double m1 = s1 / (double)cols;  // mean - x0
-    const double mean = x0 + m1;
+    const double mean = (double)x0 + m1;
     const double variance = fmax(s2 / (double)cols - m1 * m1, 0.0);
     const double factor = 1.0 / sqrt(variance + (double)eps);
     const double offset = -mean * factor;
@@ -321,17 +404,17 @@ __global__ void __launch_bounds__(512) adaln_rows(const T* x, const float* scale
       if (FULL || c < chunks) {
         opaque(raw[k]);
         float v[N], o[N];
-        Chunk<T>::unpack(raw[k], v);
+        Chunk<uint16_t>::unpack(raw[k], v);
 #pragma unroll
         for (int j = 0; j < N; ++j) {
           const float n = (float)fma((double)v[j], factor, offset);
-          const double2 t = table[j * chunks + c];
-          o[j] = (float)fma((double)n, t.x, t.y);
+          o[j] = (float)fma((double)n, a[k][j], (double)b[k][j]);
         }
-        Chunk<T>::store(out + row * cols + c * N, o);
+        Chunk<uint16_t>::store(out + row * cols + c * N, o);
       }
     }
-    if (row + stride < end) load_row(row + stride, raw);
+#pragma unroll
+    for (int k = 0; k < K; ++k) raw[k] = next[k];
   }
 }
 
@@ -443,41 +526,84 @@ int rms_norm(const char* entry, T* x, const T* y, const float* weight, T* out, i
   return launched(entry);
 }
 
-// AdaLN through adaln_rows: whole-chunk rows of at most 64 chunks per lane
-// ... 16 chunks per lane, a table that fits LDS, and enough rows per sample to
-// pay for it. Returns -1 when the shape does not qualify.
+// Waves of `kernel` (256-thread blocks) the device holds at once.
+template <typename Kernel>
+int64_t resident_waves(Kernel kernel) {
+  int device = 0, cus = 0, blocks = 0;
+  if (hipGetDevice(&device) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, kernel, 256, 0) != hipSuccess)
+    return 0;
+  return (int64_t)cus * blocks * 4;
+}
+
+template <int K, bool FULL>
+void adaln_resident_launch(const uint16_t* x, const float* scale, const float* shift, uint16_t* out, int64_t rows,
+                           int cols, int64_t rows_per_sample, int64_t samples, float eps, hipStream_t s) {
+  // every wave resident at once, rows shared out as evenly as they go
+  static std::atomic<int64_t> budget{0};
+  int64_t waves = budget.load(std::memory_order_relaxed);
+  if (waves == 0) {
+    waves = std::max<int64_t>(resident_waves(adaln_resident<K, FULL>), 4);
+    budget.store(waves, std::memory_order_relaxed);
+  }
+  int64_t per_sample = std::max<int64_t>(1, std::min(rows_per_sample, waves / samples));
+  per_sample = ceil_div(rows_per_sample, ceil_div(rows_per_sample, per_sample));
+  const dim3 grid((unsigned)ceil_div(per_sample, 4), (unsigned)samples);
+  hipLaunchKernelGGL((adaln_resident<K, FULL>), grid, dim3(256), 0, s, x, scale, shift, out, rows, cols,
+                     rows_per_sample, eps, per_sample);
+}
+
+// AdaLN: BF16 through adaln_resident, F32 through adaln_waves; rows of whole
+// 16-byte chunks, at most 4096 values. Returns -1 when the shape does not
+// qualify.
 template <typename T>
 int adaln_launch(const T* x, const float* scale, const float* shift, T* out, int64_t rows, int cols,
                  int64_t rows_per_sample, float eps, hipStream_t s) {
   constexpr int N = Chunk<T>::N;
   const int64_t samples = ceil_div(rows, rows_per_sample);
-  const size_t lds = (size_t)cols * sizeof(double2);
-  if (cols % N != 0 || lds > 64 * 1024 || rows_per_sample < 64 || samples > 65535) return -1;
+  if (cols % N != 0 || cols > kAdalnMaxCols || samples > 65535 || ceil_div(rows_per_sample, 4) >= INT32_MAX)
+    return -1;
   const int chunks = cols / N;
   const int per_lane = (int)ceil_div(chunks, kWave);
-  // about three 8-wave blocks per CU over the whole launch
-  const int64_t per_sample = std::max<int64_t>(1, std::min<int64_t>(ceil_div(rows_per_sample, 8),
-                                                                    ceil_div(3 * 256, samples)));
-  const dim3 grid((unsigned)per_sample, (unsigned)samples);
-#define DRIFT_ADALN_CASE(K)                                                                                     \
-  if (per_lane <= K) {                                                                                          \
-    if (chunks == K * kWave)                                                                                    \
-      hipLaunchKernelGGL((adaln_rows<T, K, true>), grid, dim3(512), lds, s, x, scale, shift, out, rows, cols,  \
-                         rows_per_sample, eps);                                                                 \
-    else                                                                                                        \
-      hipLaunchKernelGGL((adaln_rows<T, K, false>), grid, dim3(512), lds, s, x, scale, shift, out, rows, cols, \
-                         rows_per_sample, eps);                                                                 \
-    return 0;                                                                                                   \
+  if constexpr (sizeof(T) == 2) {
+#define DRIFT_ADALN_CASE(K)                                                                                   \
+  if (per_lane <= K) {                                                                                        \
+    if (chunks == K * kWave)                                                                                  \
+      adaln_resident_launch<K, true>(x, scale, shift, out, rows, cols, rows_per_sample, samples, eps, s);     \
+    else                                                                                                      \
+      adaln_resident_launch<K, false>(x, scale, shift, out, rows, cols, rows_per_sample, samples, eps, s);    \
+    return 0;                                                                                                 \
   }
-  DRIFT_ADALN_CASE(1)
-  DRIFT_ADALN_CASE(2)
-  DRIFT_ADALN_CASE(3)
-  DRIFT_ADALN_CASE(4)
-  DRIFT_ADALN_CASE(6)
-  DRIFT_ADALN_CASE(8)
-  DRIFT_ADALN_CASE(12)
-  DRIFT_ADALN_CASE(16)
+    DRIFT_ADALN_CASE(1)
+    DRIFT_ADALN_CASE(2)
+    DRIFT_ADALN_CASE(3)
+    DRIFT_ADALN_CASE(4)
+    DRIFT_ADALN_CASE(6)
+    DRIFT_ADALN_CASE(8)
 #undef DRIFT_ADALN_CASE
+  } else {
+    const dim3 grid((unsigned)ceil_div(rows_per_sample, 4), (unsigned)samples);
+#define DRIFT_ADALN_CASE(K)                                                                                  \
+  if (per_lane <= K) {                                                                                       \
+    if (chunks == K * kWave)                                                                                 \
+      hipLaunchKernelGGL((adaln_waves<T, K, true>), grid, dim3(256), 0, s, x, scale, shift, out, rows, cols,  \
+                         rows_per_sample, eps);                                                              \
+    else                                                                                                     \
+      hipLaunchKernelGGL((adaln_waves<T, K, false>), grid, dim3(256), 0, s, x, scale, shift, out, rows, cols, \
+                         rows_per_sample, eps);                                                              \
+    return 0;                                                                                                \
+  }
+    DRIFT_ADALN_CASE(1)
+    DRIFT_ADALN_CASE(2)
+    DRIFT_ADALN_CASE(3)
+    DRIFT_ADALN_CASE(4)
+    DRIFT_ADALN_CASE(6)
+    DRIFT_ADALN_CASE(8)
+    DRIFT_ADALN_CASE(12)
+    DRIFT_ADALN_CASE(16)
+#undef DRIFT_ADALN_CASE
+  }
   return -1;
 }
 

@@ -243,110 +243,84 @@ __global__ void __launch_bounds__(256) rope_3d_kernel(const T* x, T* out, Rope3d
   }
 }
 
-// Wan's angles depend on one axis position each, so a block makes them once
-// per (axis, position, pair of that axis) into LDS, (float cos, float sin) of
-// the double angle exactly as the host tables hold them: frames * p0 +
-// rows * p1 + cols * p2 entries (2184 for a 21 x 30 x 52 grid of 64 pairs)
-// instead of 64 sincos per token. A wave then takes a token at a time (its
-// next token's chunks already loading), looks up its pairs and turns them.
-// With a, b bf16 or F32 and c, s floats, a*c and b*s are exact in double, so
-// fma(a, c, -b*s) is the reference's a*c - b*s rounded once.
-struct AxisTables {
-  int32_t base1, base2;  // first row and column entries; frame entries start at 0
-  int32_t entries;
-  int64_t stride_mod;  // (blocks * waves) mod grid: a wave's step through the grid
-};
+// One wave per token, the grid covering the tokens in one pass. A wave issues
+// its token's loads first; while they land, each lane makes one pair's angle
+// (Wan's angle depends on one axis position: frame, row or column) and its
+// cos and sin, exactly as the host tables hold them (cos and sin of the
+// double angle, rounded to float), into the wave's LDS slice. Then each lane
+// turns its chunks' pairs. With a, b bf16 or F32 and c, s floats, a*c and b*s
+// are exact in double, so fma(a, c, -b*s) is the reference's a*c - b*s
+// rounded once.
+constexpr int kRope3dWaves = 8;
 
 template <typename T, int K, bool FIXED>
-__global__ void __launch_bounds__(512) rope_3d_axes(const T* x, T* out, Rope3dArgs p, AxisTables at) {
+__global__ void __launch_bounds__(kRope3dWaves * 64) rope_3d_waves(const T* x, T* out, Rope3dArgs p) {
   constexpr int N = Chunk<T>::N;
   using Raw = typename Chunk<T>::Raw;
-  extern __shared__ float2 axis_cs[];
-  const int p0 = p.pairs0, p1 = p.pairs1, p2 = p.dim / 2 - p0 - p1;
-  for (int e = threadIdx.x; e < at.entries; e += blockDim.x) {
-    int position, pair;
-    if (e < at.base1) {
-      position = e / p0;
-      pair = e % p0;
-    } else if (e < at.base2) {
-      position = (e - at.base1) / p1;
-      pair = p0 + (e - at.base1) % p1;
-    } else {
-      position = (e - at.base2) / p2;
-      pair = p0 + p1 + (e - at.base2) % p2;
-    }
-    double sn, cn;
-    sincos((double)position / p.denominator[pair], &sn, &cn);
-    axis_cs[e] = make_float2((float)cn, (float)sn);
-  }
-  __syncthreads();
+  __shared__ float2 cs_all[kRope3dWaves][kMaxPairs];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int waves = blockDim.x >> 6;
+  const int64_t t = (int64_t)blockIdx.x * kRope3dWaves + wave;
+  if (t >= p.tokens) return;  // no block-wide barrier follows
   const int per_token = p.heads * p.dim / N;  // chunks of a token, at most K * 64
   const int per_head = p.dim / N;
-  const int64_t stride = (int64_t)gridDim.x * waves;
-  int64_t t = (int64_t)blockIdx.x * waves + wave;
-  int64_t g = (p.token_offset + t) % p.grid;
-  const int plane = p.rows * p.cols;
+  const T* xt = x + t * p.heads * p.dim;
   // loads are never branched around (a branch makes each wait for the one
   // before): chunk indices past the token are clamped and their values unused
-  auto load_token = [&](int64_t token, Raw(&into)[K]) {
-    const T* xt = x + token * p.heads * p.dim;
-#pragma unroll
-    for (int k = 0; k < K; ++k) into[k] = Chunk<T>::load_raw(xt + min(k * kWave + lane, per_token - 1) * N);
-  };
   Raw raw[K];
-  if (t < p.tokens) load_token(t, raw);
-  for (; t < p.tokens; t += stride) {
-    Raw next[K];
-    if (t + stride < p.tokens) load_token(t + stride, next);
-    const int frame = (int)(g / plane), rem = (int)(g % plane);
-    const int base0 = frame * p0, base1 = at.base1 + (rem / p.cols) * p1, base2 = at.base2 + (rem % p.cols) * p2;
-    auto entry = [&](int m) {
-      return m < p0 ? base0 + m : (m < p0 + p1 ? base1 + m - p0 : base2 + m - p0 - p1);
-    };
-    // the lane's pairs' cos and sin, when they are the same in every chunk
-    double fc[N / 2], fs[N / 2];
-    if constexpr (FIXED) {
-      const int d0 = (lane % per_head) * N;
+#pragma unroll
+  for (int k = 0; k < K; ++k) raw[k] = Chunk<T>::load_raw(xt + min(k * kWave + lane, per_token - 1) * N);
+  const int64_t g = (p.token_offset + t) % p.grid;
+  const int plane = p.rows * p.cols;
+  const int frame = (int)(g / plane), rem = (int)(g % plane);
+  const int row = rem / p.cols, col = rem % p.cols;
+  const int half = p.dim / 2;
+  float2* cs = cs_all[wave];
+  for (int m = lane; m < half; m += kWave) {
+    const int position = m < p.pairs0 ? frame : (m < p.pairs0 + p.pairs1 ? row : col);
+    double sn, cn;
+    sincos((double)position / p.denominator[m], &sn, &cn);
+    cs[m] = make_float2((float)cn, (float)sn);
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  // the lane's pairs' cos and sin, when they are the same in every chunk
+  double fc[N / 2], fs[N / 2];
+  if constexpr (FIXED) {
+    const int m0 = (lane % per_head) * N / 2;
+#pragma unroll
+    for (int i = 0; i < N / 2; ++i) {
+      const float2 q = cs[m0 + i];
+      fc[i] = q.x;
+      fs[i] = q.y;
+    }
+  }
+  T* ot = out + t * p.heads * p.dim;
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int q = k * kWave + lane;
+    if (q < per_token) {
+      float v[N];
+      Chunk<T>::unpack(raw[k], v);
+      const int m0 = (q % per_head) * N / 2;
 #pragma unroll
       for (int i = 0; i < N / 2; ++i) {
-        const float2 q = axis_cs[entry(d0 / 2 + i)];
-        fc[i] = q.x;
-        fs[i] = q.y;
-      }
-    }
-    T* ot = out + t * p.heads * p.dim;
-#pragma unroll
-    for (int k = 0; k < K; ++k) {
-      const int q = k * kWave + lane;
-      if (q < per_token) {
-        float v[N];
-        Chunk<T>::unpack(raw[k], v);
-        const int d0 = (q % per_head) * N;
-#pragma unroll
-        for (int i = 0; i < N / 2; ++i) {
-          double c, sn;
-          if constexpr (FIXED) {
-            c = fc[i];
-            sn = fs[i];
-          } else {
-            const float2 cs = axis_cs[entry(d0 / 2 + i)];
-            c = cs.x;
-            sn = cs.y;
-          }
-          const double a = v[2 * i], b = v[2 * i + 1];
-          v[2 * i] = (float)fma(a, c, -(b * sn));
-          v[2 * i + 1] = (float)fma(a, sn, b * c);
+        double c, sn;
+        if constexpr (FIXED) {
+          c = fc[i];
+          sn = fs[i];
+        } else {
+          const float2 e = cs[m0 + i];
+          c = e.x;
+          sn = e.y;
         }
-        Chunk<T>::store(ot + q * N, v);
+        const double a = v[2 * i], b = v[2 * i + 1];
+        v[2 * i] = (float)fma(a, c, -(b * sn));
+        v[2 * i + 1] = (float)fma(a, sn, b * c);
       }
+      Chunk<T>::store(ot + q * N, v);
     }
-#pragma unroll
-    for (int k = 0; k < K; ++k) raw[k] = next[k];
-    g += at.stride_mod;
-    if (g >= p.grid) g -= p.grid;
   }
 }
 
@@ -403,92 +377,16 @@ __global__ void __launch_bounds__(256) qk_norm_rope_kernel(const T* q, const T* 
   }
 }
 
-// Whole-chunk heads with every value turning (rotary == head_dim): G lanes
-// per head, each holding two chunks (NeoX: a chunk and its partner; otherwise
-// chunks i and i + G), 64 / G heads per wave pass.
-template <typename T, int G>
-__global__ void __launch_bounds__(256) qk_norm_rope_chunks(const T* q, const T* k, T* q_out, T* k_out,
-                                                           const float* q_weight, const float* k_weight,
-                                                           const int32_t* positions, QkArgs a) {
-  constexpr int N = Chunk<T>::N;
-  constexpr int kHeadsPerPass = kWave / G;
-  __shared__ double2 cs[kMaxPairs];
-  const RopeArgs& p = a.rope;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int i0 = lane % G;  // this lane's chunks of a head: i0 and i0 + G
-  const int rows = a.q_heads + a.kv_heads;
-  const int half = p.dim / 2;
-  for (int64_t t = blockIdx.x; t < p.tokens; t += gridDim.x) {
-    token_angles(p, positions, t, cs);
-    __syncthreads();
-    for (int base = wave * kHeadsPerPass; base < rows; base += 4 * kHeadsPerPass) {
-      const int h = base + lane / G;
-      const bool live = h < rows;
-      const bool query = h < a.q_heads;
-      const T* xh = query ? q + (t * a.q_heads + h) * p.dim : k + (t * a.kv_heads + (h - a.q_heads)) * p.dim;
-      T* oh = query ? q_out + (t * a.q_heads + h) * p.dim : k_out + (t * a.kv_heads + (h - a.q_heads)) * p.dim;
-      const float* w = query ? q_weight : k_weight;
-      const int d0 = i0 * N;
-      const int d1 = (p.layout == DRIFT_ROPE_NEOX ? half : G * N) + i0 * N;
-      float a0[N], a1[N];
-      double squares = 0.0;
-      if (live) {
-        Chunk<T>::load(xh + d0, a0);
-        Chunk<T>::load(xh + d1, a1);
-#pragma unroll
-        for (int i = 0; i < N; ++i) {
-          squares = fma((double)a0[i], (double)a0[i], squares);
-          squares = fma((double)a1[i], (double)a1[i], squares);
-        }
-      }
-      squares = group_sum<G>(squares);
-      if (live) {
-        const double factor = 1.0 / sqrt(squares / (double)p.dim + (double)a.eps);
-        float w0[N], w1[N];
-#pragma unroll
-        for (int i = 0; i < N; ++i) {
-          w0[i] = w[d0 + i];
-          w1[i] = w[d1 + i];
-        }
-#pragma unroll
-        for (int i = 0; i < N; ++i) {
-          a0[i] = (float)((double)a0[i] * factor * ((double)w0[i] + (double)a.offset));
-          a1[i] = (float)((double)a1[i] * factor * ((double)w1[i] + (double)a.offset));
-        }
-        if (p.layout == DRIFT_ROPE_NEOX) {
-#pragma unroll
-          for (int i = 0; i < N; ++i) {
-            const double2 c = cs[d0 + i];
-            turn(a0[i], a1[i], c.x, c.y, a0[i], a1[i]);
-          }
-        } else {
-#pragma unroll
-          for (int i = 0; i < N; i += 2) {
-            const double2 c0 = cs[(d0 + i) / 2], c1 = cs[(d1 + i) / 2];
-            turn(a0[i], a0[i + 1], c0.x, c0.y, a0[i], a0[i + 1]);
-            turn(a1[i], a1[i + 1], c1.x, c1.y, a1[i], a1[i + 1]);
-          }
-        }
-        Chunk<T>::store(oh + d0, a0);
-        Chunk<T>::store(oh + d1, a1);
-      }
-    }
-    __syncthreads();  // cs is remade for the next token
-  }
-}
-
-// The fast path for whole-chunk heads with every value turning, one wave per
-// token: the token's pairs' cos and sin (one sincos per lane) into the wave's
-// LDS slice, the norm weights (+ offset, in double) into LDS once per block;
-// then passes of 64 / G heads, G lanes per head each holding two chunks (NeoX:
-// a chunk and its partner; otherwise chunks i and i + G), every pass's loads
-// issued before the first pass computes.
+// The fast path for whole-chunk heads with every value turning: one block per
+// token, G lanes per head, each lane holding two chunks of its head (NeoX: a
+// chunk and its partner; otherwise chunks i and i + G), 64 / G heads per
+// wave. The grid covers the tokens in one pass. Each lane issues its loads
+// first; while they land the block makes the token's cos and sin (one sincos
+// per pair) and the norm weights (+ offset, in double) into LDS.
 //
 // LDS is laid out so the G lanes of a head read consecutive entries: for NeoX
 // the pair (and weight) of lane i0's value i sits at i * G + i0 (the natural
-// index would put the G lanes 128 bytes apart, on the same banks). Each pass
-// re-reads its angles and weights from LDS rather than keeping them in
-// registers, which keeps every token's wave resident in one round.
+// index would put the G lanes N entries apart, on the same banks).
 template <bool NEOX, int G, int N>
 __device__ __forceinline__ int qk_pair_slot(int pair) {
   if constexpr (NEOX) return (pair % N) * G + pair / N;
@@ -505,104 +403,105 @@ __device__ __forceinline__ int qk_weight_slot(int d) {
   return d;
 }
 
+constexpr int kQkMaxWaves = 16;
+
 template <typename T, int G, bool NEOX>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) qk_norm_rope_waves(const T* q, const T* k, T* q_out, T* k_out,
-                                                          const float* q_weight, const float* k_weight,
-                                                          const int32_t* positions, QkArgs a) {
+__global__ void __launch_bounds__(kQkMaxWaves * 64) qk_norm_rope_token(const T* q, const T* k, T* q_out, T* k_out,
+                                                                     const float* q_weight, const float* k_weight,
+                                                                     const int32_t* positions, QkArgs a) {
   constexpr int N = Chunk<T>::N;
   using Raw = typename Chunk<T>::Raw;
-  constexpr int kHeadsPerPass = kWave / G;
-  constexpr int kMaxPasses = 5;
+  constexpr int kHeadsPerWave = kWave / G;
   constexpr int kPairs = N * G;  // a head's pairs (rotary == dim == 2 N G)
-  __shared__ double2 cs_all[4][kPairs];
+  __shared__ double2 cs[kPairs];
   __shared__ double weights[2][2 * kPairs];
   const RopeArgs& p = a.rope;
-  const int dim = 2 * N * G, half = N * G;
-  for (int d = threadIdx.x; d < dim; d += blockDim.x) {
-    const int slot = qk_weight_slot<NEOX, G, N>(d);
-    weights[0][slot] = (double)q_weight[d] + (double)a.offset;
-    weights[1][slot] = (double)k_weight[d] + (double)a.offset;
+  constexpr int dim = 2 * N * G, half = N * G;
+  const int64_t t = blockIdx.x;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int waves = blockDim.x >> 6;
+  const int rows = a.q_heads + a.kv_heads;
+  const int i0 = lane % G;
+  const int d0 = i0 * N, d1 = (NEOX ? half : G * N) + i0 * N;
+  auto head_at = [&](auto* qs, auto* ks, int h) {
+    return h < a.q_heads ? qs + (t * a.q_heads + h) * dim : ks + (t * a.kv_heads + (h - a.q_heads)) * dim;
+  };
+  // the angles' and weights' operands load first: a wave's loads complete in
+  // issue order, so the tables are made while the heads are still loading
+  const int j = threadIdx.x;
+  int32_t position = 0;
+  float qw = 0.0f, kw = 0.0f;
+  if (j < half) position = positions[(int64_t)rope_section(j, p) * p.tokens + t];
+  if (j < dim) {
+    qw = q_weight[j];
+    kw = k_weight[j];
+  }
+  int h = wave * kHeadsPerWave + lane / G;
+  Raw r0, r1;
+  if (h < rows) {
+    const T* xh = head_at(q, k, h);
+    r0 = Chunk<T>::load_raw(xh + d0);
+    r1 = Chunk<T>::load_raw(xh + d1);
+  }
+  if (j < half) {
+    double sn, cn;
+    sincos((double)((float)position * p.inverse[j]), &sn, &cn);
+    cs[qk_pair_slot<NEOX, G, N>(j)] = make_double2(cn, sn);
+  }
+  if (j < dim) {
+    const int slot = qk_weight_slot<NEOX, G, N>(j);
+    weights[0][slot] = (double)qw + (double)a.offset;
+    weights[1][slot] = (double)kw + (double)a.offset;
   }
   __syncthreads();
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  double2* cs = cs_all[wave];
-  const int rows = a.q_heads + a.kv_heads;
-  const int passes = (rows + kHeadsPerPass - 1) / kHeadsPerPass;
-  const int i0 = lane % G;
-  const int d0 = i0 * N, d1 = half + i0 * N;
-  for (int64_t t = (int64_t)blockIdx.x * 4 + wave; t < p.tokens; t += (int64_t)gridDim.x * 4) {
-    for (int first = 0; first < passes; first += kMaxPasses) {
-      Raw r0[kMaxPasses], r1[kMaxPasses];
+  for (;;) {
+    const bool live = h < rows;
+    float v0[N], v1[N];
+    double squares = 0.0;
+    if (live) {
+      Chunk<T>::unpack(r0, v0);
+      Chunk<T>::unpack(r1, v1);
 #pragma unroll
-      for (int s = 0; s < kMaxPasses; ++s) {
-        if (first + s < passes) {
-          // a head past the last is clamped to it: loads are never branched around
-          const int h = min((first + s) * kHeadsPerPass + lane / G, rows - 1);
-          const T* xh = h < a.q_heads ? q + (t * a.q_heads + h) * dim : k + (t * a.kv_heads + (h - a.q_heads)) * dim;
-          r0[s] = Chunk<T>::load_raw(xh + d0);
-          r1[s] = Chunk<T>::load_raw(xh + d1);
-        }
-      }
-      if (first == 0) {
-        // the token's angles, made while its heads load
-        for (int j = lane; j < half; j += kWave) {
-          const int32_t position = positions[(int64_t)rope_section(j, p) * p.tokens + t];
-          double sn, cn;
-          sincos((double)((float)position * p.inverse[j]), &sn, &cn);
-          cs[qk_pair_slot<NEOX, G, N>(j)] = make_double2(cn, sn);
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      }
-#pragma unroll
-      for (int s = 0; s < kMaxPasses; ++s) {
-        if (first + s >= passes) break;
-        asm volatile("" ::: "memory");  // angles and weights are re-read from LDS each pass
-        const int h = (first + s) * kHeadsPerPass + lane / G;
-        const bool query = h < a.q_heads;
-        float v0[N], v1[N];
-        Chunk<T>::unpack(r0[s], v0);
-        Chunk<T>::unpack(r1[s], v1);
-        double squares = 0.0;
-#pragma unroll
-        for (int i = 0; i < N; ++i) {
-          squares = fma((double)v0[i], (double)v0[i], squares);
-          squares = fma((double)v1[i], (double)v1[i], squares);
-        }
-        squares = group_sum<G>(squares);
-        if (h < rows) {
-          const double factor = 1.0 / sqrt(squares / (double)dim + (double)a.eps);
-          const double* w = weights[query ? 0 : 1];
-#pragma unroll
-          for (int i = 0; i < N; ++i) {
-            v0[i] = (float)((double)v0[i] * factor * w[qk_weight_slot<NEOX, G, N>(d0 + i)]);
-            v1[i] = (float)((double)v1[i] * factor * w[qk_weight_slot<NEOX, G, N>(d1 + i)]);
-          }
-          if constexpr (NEOX) {
-#pragma unroll
-            for (int i = 0; i < N; ++i) {
-              const double2 c = cs[qk_pair_slot<NEOX, G, N>(d0 + i)];
-              turn_fused(v0[i], v1[i], c.x, c.y, v0[i], v1[i]);
-            }
-          } else {
-#pragma unroll
-            for (int i = 0; i < N; i += 2) {
-              const double2 c0 = cs[(d0 + i) / 2], c1 = cs[(d1 + i) / 2];
-              turn_fused(v0[i], v0[i + 1], c0.x, c0.y, v0[i], v0[i + 1]);
-              turn_fused(v1[i], v1[i + 1], c1.x, c1.y, v1[i], v1[i + 1]);
-            }
-          }
-          T* oh = query ? q_out + (t * a.q_heads + h) * dim : k_out + (t * a.kv_heads + (h - a.q_heads)) * dim;
-          Chunk<T>::store(oh + d0, v0);
-          Chunk<T>::store(oh + d1, v1);
-        }
+      for (int i = 0; i < N; ++i) {
+        squares = fma((double)v0[i], (double)v0[i], squares);
+        squares = fma((double)v1[i], (double)v1[i], squares);
       }
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();  // cs is remade for the next token
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    squares = group_sum<G>(squares);
+    if (live) {
+      const double factor = 1.0 / sqrt(squares / (double)dim + (double)a.eps);
+      const double* w = weights[h < a.q_heads ? 0 : 1];
+#pragma unroll
+      for (int i = 0; i < N; ++i) {
+        v0[i] = (float)((double)v0[i] * factor * w[qk_weight_slot<NEOX, G, N>(d0 + i)]);
+        v1[i] = (float)((double)v1[i] * factor * w[qk_weight_slot<NEOX, G, N>(d1 + i)]);
+      }
+      if constexpr (NEOX) {
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+          const double2 c = cs[qk_pair_slot<NEOX, G, N>(d0 + i)];
+          turn_fused(v0[i], v1[i], c.x, c.y, v0[i], v1[i]);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < N; i += 2) {
+          const double2 c0 = cs[(d0 + i) / 2], c1 = cs[(d1 + i) / 2];
+          turn_fused(v0[i], v0[i + 1], c0.x, c0.y, v0[i], v0[i + 1]);
+          turn_fused(v1[i], v1[i + 1], c1.x, c1.y, v1[i], v1[i + 1]);
+        }
+      }
+      T* oh = head_at(q_out, k_out, h);
+      Chunk<T>::store(oh + d0, v0);
+      Chunk<T>::store(oh + d1, v1);
+    }
+    // more heads than the block has waves for: the next pass of this wave
+    h += waves * kHeadsPerWave;
+    if (h - lane / G >= rows) break;
+    if (h < rows) {
+      const T* xh = head_at(q, k, h);
+      r0 = Chunk<T>::load_raw(xh + d0);
+      r1 = Chunk<T>::load_raw(xh + d1);
+    }
   }
 }
 
@@ -734,24 +633,18 @@ int rope_3d(const char* entry, const T* x, T* out, int64_t tokens, int32_t heads
   constexpr int N = Chunk<T>::N;
   const bool chunked = aligned16(x) && aligned16(out) && dim % N == 0;
   const hipStream_t st = (hipStream_t)stream;
-  const int64_t entries = (int64_t)frames * axes[0] + (int64_t)rows * axes[1] + (int64_t)cols * axes[2];
-  if (chunked && entries * (int64_t)sizeof(float2) <= 64 * 1024) {
-    AxisTables at;
-    at.base1 = frames * axes[0];
-    at.base2 = at.base1 + rows * axes[1];
-    at.entries = (int32_t)entries;
-    const int waves = 8;
-    const unsigned blocks = (unsigned)std::min<int64_t>(ceil_div(tokens, waves), 2048);
-    at.stride_mod = ((int64_t)blocks * waves) % p.grid;
-    const size_t lds = (size_t)entries * sizeof(float2);
-    const int per_lane = (int)ceil_div((int64_t)heads * dim / N, kWave);
+  const int per_lane = (int)ceil_div((int64_t)heads * dim / N, kWave);
+  const int64_t blocks = ceil_div(tokens, kRope3dWaves);
+  if (chunked && blocks <= kOneShotBlocks) {
     const bool fixed = (64 % (dim / N)) == 0;
 #define DRIFT_ROPE3D_CASE(K)                                                                                  \
   if (per_lane <= K) {                                                                                        \
     if (fixed)                                                                                                \
-      hipLaunchKernelGGL((rope_3d_axes<T, K, true>), dim3(blocks), dim3(64 * waves), lds, st, x, out, p, at);  \
+      hipLaunchKernelGGL((rope_3d_waves<T, K, true>), dim3((unsigned)blocks), dim3(64 * kRope3dWaves), 0, st, \
+                         x, out, p);                                                                          \
     else                                                                                                      \
-      hipLaunchKernelGGL((rope_3d_axes<T, K, false>), dim3(blocks), dim3(64 * waves), lds, st, x, out, p, at); \
+      hipLaunchKernelGGL((rope_3d_waves<T, K, false>), dim3((unsigned)blocks), dim3(64 * kRope3dWaves), 0,    \
+                         st, x, out, p);                                                                      \
     return launched(entry);                                                                                   \
   }
     DRIFT_ROPE3D_CASE(1)
@@ -797,16 +690,20 @@ int qk_norm_rope(const char* entry, const T* q, const T* k, T* q_out, T* k_out, 
   const dim3 grid(grid_for(tokens, 1, 1 << 16));
   const hipStream_t st = (hipStream_t)stream;
   if (whole) {
-    const dim3 waves_grid(grid_for(tokens, 4, 1 << 16));
+    const int heads_per_wave = kWave / lanes_per_head;
+    // a wave per 64 / G heads, and a thread per weight of a head
+    const int waves = (int)std::min<int64_t>(
+        kQkMaxWaves, std::max<int64_t>(ceil_div(heads + kv_heads, heads_per_wave), ceil_div(dim, kWave)));
+    const dim3 block(64 * waves);
     switch (lanes_per_head) {
-#define DRIFT_QK_CASE(G)                                                                                    \
-  case G:                                                                                                   \
-    if (layout == DRIFT_ROPE_NEOX)                                                                          \
-      hipLaunchKernelGGL((qk_norm_rope_waves<T, G, true>), waves_grid, dim3(256), 0, st, q, k, q_out, k_out,  \
-                         q_weight, k_weight, positions, a);                                                 \
-    else                                                                                                    \
-      hipLaunchKernelGGL((qk_norm_rope_waves<T, G, false>), waves_grid, dim3(256), 0, st, q, k, q_out, k_out, \
-                         q_weight, k_weight, positions, a);                                                 \
+#define DRIFT_QK_CASE(G)                                                                                         \
+  case G:                                                                                                        \
+    if (layout == DRIFT_ROPE_NEOX)                                                                               \
+      hipLaunchKernelGGL((qk_norm_rope_token<T, G, true>), dim3(tokens), block, 0, st, q, k, q_out, k_out,       \
+                         q_weight, k_weight, positions, a);                                                      \
+    else                                                                                                         \
+      hipLaunchKernelGGL((qk_norm_rope_token<T, G, false>), dim3(tokens), block, 0, st, q, k, q_out, k_out,      \
+                         q_weight, k_weight, positions, a);                                                      \
     break;
       DRIFT_QK_CASE(1)
       DRIFT_QK_CASE(2)
