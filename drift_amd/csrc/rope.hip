@@ -428,24 +428,19 @@ __global__ void __launch_bounds__(kQkMaxWaves * 64) qk_norm_rope_token(const T* 
   };
   // the angles' and weights' operands load first: a wave's loads complete in
   // issue order, so the tables are made while the heads are still loading
-  const int j = threadIdx.x;
-  int32_t position = 0;
-  float qw = 0.0f, kw = 0.0f;
-  if (j < half) position = positions[(int64_t)rope_section(j, p) * p.tokens + t];
-  if (j < dim) {
-    qw = q_weight[j];
-    kw = k_weight[j];
-  }
+  const int j = threadIdx.x, jp = min(j, half - 1), jd = min(j, dim - 1);
+  const int32_t position = positions[(int64_t)rope_section(jp, p) * p.tokens + t];
+  const float inverse = p.inverse[jp];
+  const float qw = q_weight[jd], kw = k_weight[jd];
+  // loads are never branched around (the wait for the angles' operands would
+  // then wait for them too): a head past the last is clamped to it
   int h = wave * kHeadsPerWave + lane / G;
-  Raw r0, r1;
-  if (h < rows) {
-    const T* xh = head_at(q, k, h);
-    r0 = Chunk<T>::load_raw(xh + d0);
-    r1 = Chunk<T>::load_raw(xh + d1);
-  }
+  const T* xh = head_at(q, k, min(h, rows - 1));
+  Raw r0 = Chunk<T>::load_raw(xh + d0);
+  Raw r1 = Chunk<T>::load_raw(xh + d1);
   if (j < half) {
     double sn, cn;
-    sincos((double)((float)position * p.inverse[j]), &sn, &cn);
+    sincos((double)((float)position * inverse), &sn, &cn);
     cs[qk_pair_slot<NEOX, G, N>(j)] = make_double2(cn, sn);
   }
   if (j < dim) {
@@ -497,11 +492,9 @@ __global__ void __launch_bounds__(kQkMaxWaves * 64) qk_norm_rope_token(const T* 
     // more heads than the block has waves for: the next pass of this wave
     h += waves * kHeadsPerWave;
     if (h - lane / G >= rows) break;
-    if (h < rows) {
-      const T* xh = head_at(q, k, h);
-      r0 = Chunk<T>::load_raw(xh + d0);
-      r1 = Chunk<T>::load_raw(xh + d1);
-    }
+    xh = head_at(q, k, min(h, rows - 1));
+    r0 = Chunk<T>::load_raw(xh + d0);
+    r1 = Chunk<T>::load_raw(xh + d1);
   }
 }
 
