@@ -456,20 +456,22 @@ def main():
             k.fire(i)
     torch.cuda.synchronize()
 
+    # One event pair on the launch stream around each kernel's K back-to-back
+    # launches: the average launch duration is their span over K (a pair per
+    # launch would add the event's own dispatch to every launch, a few us).
     stream = torch.cuda.current_stream()
-    events = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-               for _ in range(args.steps)] for _ in kernels]
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in kernels]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for k, pairs in zip(kernels, events):
-        for i, (start, end) in enumerate(pairs):
-            start.record(stream)
+    for k, (start, end) in zip(kernels, events):
+        start.record(stream)
+        for i in range(args.steps):
             k.fire(args.warmup + i)
-            end.record(stream)
+        end.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    for k, pairs in zip(kernels, events):
-        k.times_ms = [start.elapsed_time(end) for start, end in pairs]
+    for k, (start, end) in zip(kernels, events):
+        k.times_ms = [start.elapsed_time(end) / args.steps]
 
     # The practical HBM ceiling on this box, measured in the same run: a plain
     # device copy of one C5 tensor (402.6 MB read + 402.6 MB written) into
@@ -481,15 +483,13 @@ def main():
     for i in range(2):
         dsts[i].copy_(src)
     torch.cuda.synchronize()
-    copy_events = []
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
     for i in range(10):
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        start.record(stream)
         dsts[i % 2].copy_(src)
-        end.record(stream)
-        copy_events.append((start, end))
+    end.record(stream)
     torch.cuda.synchronize()
-    copy_ms = float(np.mean([s.elapsed_time(e) for s, e in copy_events]))
+    copy_ms = start.elapsed_time(end) / 10
     copy_gbs = 2 * copy_elems * 2 / (copy_ms * 1e-3) / 1e9
     del src, dsts
 
