@@ -56,12 +56,22 @@ SIGNATURES = {
                                       _I32, _I32, _I32, _I32, _I32, _I32, _P]),
     "drift_qk_norm_rope_bf16": (_I32, [_P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _F32, _F32, _I32, _F32,
                                        _I32, _I32, _I32, _I32, _I32, _I32, _P]),
+    "drift_cache_write_f32": (_I32, [_P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _P, _P]),
+    "drift_cache_write_bf16": (_I32, [_P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _P, _P]),
+    "drift_split_halves_f32": (_I32, [_P, _P, _P, _I64, _I32, _P]),
+    "drift_split_halves_bf16": (_I32, [_P, _P, _P, _I64, _I32, _P]),
+    "drift_attention_inputs_f32": (_I32, [_P, _P, _P, _P, _P, _F32, _F32, _P, _I32, _I32, _I32, _I32, _I32, _F32,
+                                          _I32, _I32, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _P, _I32, _I32, _I32,
+                                          _I32, _P, _P]),
+    "drift_attention_inputs_bf16": (_I32, [_P, _P, _P, _P, _P, _F32, _F32, _P, _I32, _I32, _I32, _I32, _I32, _F32,
+                                           _I32, _I32, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _P, _I32, _I32, _I32,
+                                           _I32, _P, _P]),
     "drift_embedding_q8_0_f32": (_I32, [_P, _P, _P, _I64, _I64, _I32, _P, _P]),
     "drift_embedding_q8_0_bf16": (_I32, [_P, _P, _P, _I64, _I64, _I32, _P, _P]),
     "drift_convert": (_I32, [_P, _P, _I64, _I32, _P]),
 }
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 
 class NotBuilt(RuntimeError):

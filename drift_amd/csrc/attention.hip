@@ -1,0 +1,617 @@
+// Attention inputs for gfx950: per-head query/key RMSNorm fused with rope,
+// the same with a gated query's split and the keys' and values' write into
+// the runner's paged F16 KV cache (attention_inputs), the cache write alone,
+// and the split of a row's halves.
+//
+// Layouts: queries and keys [tokens, heads, head_dim] row-major (a gated
+// query projection [tokens, heads, 2 head_dim]: the query, then its output
+// gate). The cache (ops/KvCache.scala:5-22): keys F16 [pages, page_size,
+// kv_heads, head_dim], values F16 [pages, kv_heads, head_dim, page_size]
+// (transposed within a page); a sequence's page table (int32) maps
+// position / page_size to a page.
+//
+// Arithmetic is the CPU reference's: the norm in double rounded once to F32
+// (rmsNorm writes F32), the rope of those F32 values (ops/CpuAttention.scala:
+// 89-146, as rope.hpp), and F32 -> F16 rounding to nearest even for the
+// cache (Float.floatToFloat16 in ops/CpuAttention.scala:181-210).
+#include "rope.hpp"
+
+#include <algorithm>
+#include <climits>
+
+namespace drift {
+namespace {
+
+// ------------------------------------------------------------------ per-head RMSNorm + rope
+
+struct QkArgs {
+  RopeArgs rope;
+  int32_t q_heads, kv_heads;
+  float eps, offset;
+  int64_t q_stride;  // values from one query head's row to the next: head_dim, or 2 head_dim with a gate
+};
+
+// What attention_inputs writes beyond the rotated queries: the gate half of
+// each query head's row (when `gate` is set) and, when `keys` is set, the
+// rotated keys and the values `v` into the paged cache instead of k_out.
+template <typename T>
+struct Extras {
+  T* gate;
+  const T* v;
+  uint16_t* keys;    // F16 [pages, page_size, kv_heads, head_dim]
+  uint16_t* values;  // F16 [pages, kv_heads, head_dim, page_size]
+  const int32_t* page_table;
+  int32_t pages, page_size, start;
+  int32_t* bad_page;
+};
+
+// Token t's place in the cache for key head kv: keys[key + d] and
+// values[value + d * page_size] (ops/CpuAttention.scala:163-179). False
+// when the page table names a page outside the cache: then nothing is
+// written and *bad_page is set.
+template <typename T>
+__device__ __forceinline__ bool cache_place(const Extras<T>& e, int64_t t, int kv_heads, int dim, int kv,
+                                            int64_t& key, int64_t& value) {
+  const int64_t position = e.start + t;
+  const int64_t page = e.page_table[position / e.page_size];
+  const int64_t offset = position % e.page_size;
+  if (page < 0 || page >= e.pages) {
+    if (e.bad_page) *e.bad_page = 1;
+    return false;
+  }
+  key = ((page * e.page_size + offset) * kv_heads + kv) * dim;
+  value = (page * kv_heads + kv) * (int64_t)dim * e.page_size + offset;
+  return true;
+}
+
+// F32 -> F16 bits, to nearest even (v_cvt_f16_f32): Float.floatToFloat16's
+// rounding; NaN payloads are the hardware's.
+__device__ __forceinline__ uint32_t f16_bits(float v) { return __builtin_bit_cast(uint16_t, (_Float16)v); }
+
+// N consecutive values as F16, one 8- or 16-byte store.
+template <int N>
+__device__ __forceinline__ void store_f16(uint16_t* p, const float (&v)[N]) {
+  uint32_t w[N / 2];
+#pragma unroll
+  for (int i = 0; i < N / 2; ++i) w[i] = f16_bits(v[2 * i]) | (f16_bits(v[2 * i + 1]) << 16);
+  if constexpr (N == 8)
+    *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+  else
+    *reinterpret_cast<uint2*>(p) = make_uint2(w[0], w[1]);
+}
+
+// Any head size: each wave norms one head row at a time into LDS (the F32
+// values rmsNorm writes), then turns its pairs from there. With EXTRAS, the
+// gate half of a query row is copied out, and a key head's turned row and
+// its values go to the cache as F16.
+template <typename T, bool EXTRAS>
+__global__ void __launch_bounds__(256) qk_norm_rope_kernel(const T* q, const T* k, T* q_out, T* k_out,
+                                                           const float* q_weight, const float* k_weight,
+                                                           const int32_t* positions, QkArgs a, Extras<T> e) {
+  __shared__ double2 cs[kMaxPairs];
+  __shared__ float normed[4][2 * kMaxPairs];
+  const RopeArgs& p = a.rope;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int rows = a.q_heads + a.kv_heads;
+  const int slots = (p.dim + 1) / 2;
+  for (int64_t t = blockIdx.x; t < p.tokens; t += gridDim.x) {
+    token_angles(p, positions, t, cs);
+    for (int round = 0; round < rows; round += 4) {
+      const int h = round + wave;
+      const bool query = h < a.q_heads;
+      const int kv = h - a.q_heads;
+      const T* xh = query ? q + (t * a.q_heads + h) * a.q_stride : k + (t * a.kv_heads + kv) * p.dim;
+      const float* w = query ? q_weight : k_weight;
+      if (h < rows) {
+        float v[2 * kMaxPairs / kWave];
+        double squares = 0.0;
+#pragma unroll
+        for (int i = 0; i < 2 * kMaxPairs / kWave; ++i) {
+          const int d = i * kWave + lane;
+          v[i] = d < p.dim ? load_one(xh + d) : 0.0f;
+          squares = fma((double)v[i], (double)v[i], squares);
+        }
+        if (EXTRAS && query && e.gate)
+          for (int d = lane; d < p.dim; d += kWave)
+            store_one(e.gate + (t * a.q_heads + h) * p.dim + d, load_one(xh + p.dim + d));
+        const double factor = 1.0 / sqrt(group_sum<64>(squares) / (double)p.dim + (double)a.eps);
+#pragma unroll
+        for (int i = 0; i < 2 * kMaxPairs / kWave; ++i) {
+          const int d = i * kWave + lane;
+          if (d < p.dim) normed[wave][d] = (float)((double)v[i] * factor * ((double)w[d] + (double)a.offset));
+        }
+      }
+      __syncthreads();  // normed rows and (first round) cs are ready
+      if (h < rows) {
+        auto load = [&](int d) { return (double)normed[wave][d]; };
+        if (!EXTRAS || query || !e.keys) {
+          T* oh = query ? q_out + (t * a.q_heads + h) * p.dim : k_out + (t * a.kv_heads + kv) * p.dim;
+          for (int j = lane; j < slots; j += kWave) turn_slot<T>(j, p.dim, p.rotary, p.layout, cs, load, oh);
+        } else {
+          int64_t key, value;
+          if (cache_place(e, t, a.kv_heads, p.dim, kv, key, value)) {
+            for (int j = lane; j < slots; j += kWave)
+              turn_slot(j, p.dim, p.rotary, p.layout, cs, load,
+                        [&](int d, float r) { e.keys[key + d] = (uint16_t)f16_bits(r); });
+            const T* vh = e.v + (t * a.kv_heads + kv) * p.dim;
+            for (int d = lane; d < p.dim; d += kWave)
+              e.values[value + (int64_t)d * e.page_size] = (uint16_t)f16_bits(load_one(vh + d));
+          }
+        }
+      }
+      __syncthreads();  // normed is reused next round, cs next token
+    }
+  }
+}
+
+// The fast path for whole-chunk heads with every value turning: one block per
+// token, G lanes per head, each lane holding two chunks of its head (NeoX: a
+// chunk and its partner; otherwise chunks i and i + G), 64 / G heads per
+// wave. The grid covers the tokens in one pass. Each lane issues its loads
+// first; while they land the block makes the token's cos and sin (one sincos
+// per pair) and the norm weights (+ offset, in double) into LDS.
+//
+// LDS is laid out so the G lanes of a head read consecutive entries: for NeoX
+// the pair (and weight) of lane i0's value i sits at i * G + i0 (the natural
+// index would put the G lanes N entries apart, on the same banks).
+template <bool NEOX, int G, int N>
+__device__ __forceinline__ int qk_pair_slot(int pair) {
+  if constexpr (NEOX) return (pair % N) * G + pair / N;
+  return pair;
+}
+
+template <bool NEOX, int G, int N>
+__device__ __forceinline__ int qk_weight_slot(int d) {
+  if constexpr (NEOX) {
+    const int half = N * G;
+    const int h = d >= half ? 1 : 0, e = d - h * half;
+    return h * half + (e % N) * G + e / N;
+  }
+  return d;
+}
+
+constexpr int kQkMaxWaves = 16;
+
+template <typename T, int G, bool NEOX, bool EXTRAS>
+__global__ void __launch_bounds__(kQkMaxWaves * 64) qk_norm_rope_token(const T* q, const T* k, T* q_out, T* k_out,
+                                                                     const float* q_weight, const float* k_weight,
+                                                                     const int32_t* positions, QkArgs a,
+                                                                     Extras<T> e) {
+  constexpr int N = Chunk<T>::N;
+  using Raw = typename Chunk<T>::Raw;
+  constexpr int kHeadsPerWave = kWave / G;
+  constexpr int kPairs = N * G;  // a head's pairs (rotary == dim == 2 N G)
+  __shared__ double2 cs[kPairs];
+  __shared__ double weights[2][2 * kPairs];
+  const RopeArgs& p = a.rope;
+  constexpr int dim = 2 * N * G, half = N * G;
+  const int64_t t = blockIdx.x;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int waves = blockDim.x >> 6;
+  const int rows = a.q_heads + a.kv_heads;
+  const int i0 = lane % G;
+  const int d0 = i0 * N, d1 = (NEOX ? half : G * N) + i0 * N;
+  auto head_at = [&](auto* qs, auto* ks, int h) {
+    return h < a.q_heads ? qs + (t * a.q_heads + h) * dim : ks + (t * a.kv_heads + (h - a.q_heads)) * dim;
+  };
+  auto input_at = [&](int h) {
+    return h < a.q_heads ? q + (t * a.q_heads + h) * a.q_stride : k + (t * a.kv_heads + (h - a.q_heads)) * dim;
+  };
+  // the angles' and weights' operands load first: a wave's loads complete in
+  // issue order, so the tables are made while the heads are still loading
+  const int j = threadIdx.x, jp = min(j, half - 1), jd = min(j, dim - 1);
+  const int32_t position = positions[(int64_t)rope_section(jp, p) * p.tokens + t];
+  const float inverse = p.inverse[jp];
+  const float qw = q_weight[jd], kw = k_weight[jd];
+  // loads are never branched around (the wait for the angles' operands would
+  // then wait for them too): a head past the last is clamped to it
+  int h = wave * kHeadsPerWave + lane / G;
+  const T* xh = input_at(min(h, rows - 1));
+  Raw r0 = Chunk<T>::load_raw(xh + d0);
+  Raw r1 = Chunk<T>::load_raw(xh + d1);
+  // the gate half of a query head's row; the values of a key head's (rows
+  // past the last of their kind are clamped to it)
+  Raw g0, g1, u0, u1;
+  auto load_extras = [&](int hh) {
+    if (e.gate && a.q_heads > 0) {
+      const T* gh = q + (t * a.q_heads + min(hh, a.q_heads - 1)) * a.q_stride + dim;
+      g0 = Chunk<T>::load_raw(gh + d0);
+      g1 = Chunk<T>::load_raw(gh + d1);
+    }
+    if (e.keys && a.kv_heads > 0) {
+      const T* vh = e.v + (t * a.kv_heads + min(max(hh - a.q_heads, 0), a.kv_heads - 1)) * dim;
+      u0 = Chunk<T>::load_raw(vh + d0);
+      u1 = Chunk<T>::load_raw(vh + d1);
+    }
+  };
+  if constexpr (EXTRAS) load_extras(h);
+  if (j < half) {
+    double sn, cn;
+    sincos((double)((float)position * inverse), &sn, &cn);
+    cs[qk_pair_slot<NEOX, G, N>(j)] = make_double2(cn, sn);
+  }
+  if (j < dim) {
+    const int slot = qk_weight_slot<NEOX, G, N>(j);
+    weights[0][slot] = (double)qw + (double)a.offset;
+    weights[1][slot] = (double)kw + (double)a.offset;
+  }
+  __syncthreads();
+  for (;;) {
+    const bool live = h < rows;
+    float v0[N], v1[N];
+    double squares = 0.0;
+    if (live) {
+      Chunk<T>::unpack(r0, v0);
+      Chunk<T>::unpack(r1, v1);
+#pragma unroll
+      for (int i = 0; i < N; ++i) {
+        squares = fma((double)v0[i], (double)v0[i], squares);
+        squares = fma((double)v1[i], (double)v1[i], squares);
+      }
+    }
+    squares = group_sum<G>(squares);
+    if (live) {
+      const double factor = 1.0 / sqrt(squares / (double)dim + (double)a.eps);
+      const double* w = weights[h < a.q_heads ? 0 : 1];
+#pragma unroll
+      for (int i = 0; i < N; ++i) {
+        v0[i] = (float)((double)v0[i] * factor * w[qk_weight_slot<NEOX, G, N>(d0 + i)]);
+        v1[i] = (float)((double)v1[i] * factor * w[qk_weight_slot<NEOX, G, N>(d1 + i)]);
+      }
+      if constexpr (NEOX) {
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+          const double2 c = cs[qk_pair_slot<NEOX, G, N>(d0 + i)];
+          turn_fused(v0[i], v1[i], c.x, c.y, v0[i], v1[i]);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < N; i += 2) {
+          const double2 c0 = cs[(d0 + i) / 2], c1 = cs[(d1 + i) / 2];
+          turn_fused(v0[i], v0[i + 1], c0.x, c0.y, v0[i], v0[i + 1]);
+          turn_fused(v1[i], v1[i + 1], c1.x, c1.y, v1[i], v1[i + 1]);
+        }
+      }
+      const bool query = h < a.q_heads;
+      if (!EXTRAS || query || !e.keys) {
+        T* oh = head_at(q_out, k_out, h);
+        Chunk<T>::store(oh + d0, v0);
+        Chunk<T>::store(oh + d1, v1);
+      }
+      if constexpr (EXTRAS) {
+        if (query && e.gate) {
+          T* gh = e.gate + (t * a.q_heads + h) * dim;
+          *reinterpret_cast<uint4*>(gh + d0) = g0;
+          *reinterpret_cast<uint4*>(gh + d1) = g1;
+        }
+        int64_t key, value;
+        if (!query && e.keys && cache_place(e, t, a.kv_heads, dim, h - a.q_heads, key, value)) {
+          store_f16<N>(e.keys + key + d0, v0);
+          store_f16<N>(e.keys + key + d1, v1);
+          float w0[N], w1[N];
+          Chunk<T>::unpack(u0, w0);
+          Chunk<T>::unpack(u1, w1);
+#pragma unroll
+          for (int i = 0; i < N; ++i) {
+            e.values[value + (int64_t)(d0 + i) * e.page_size] = (uint16_t)f16_bits(w0[i]);
+            e.values[value + (int64_t)(d1 + i) * e.page_size] = (uint16_t)f16_bits(w1[i]);
+          }
+        }
+      }
+    }
+    // more heads than the block has waves for: the next pass of this wave
+    h += waves * kHeadsPerWave;
+    if (h - lane / G >= rows) break;
+    xh = input_at(min(h, rows - 1));
+    r0 = Chunk<T>::load_raw(xh + d0);
+    r1 = Chunk<T>::load_raw(xh + d1);
+    if constexpr (EXTRAS) load_extras(h);
+  }
+}
+
+// ------------------------------------------------------------------ cache write, split halves
+
+// Keys and values [tokens, kv_heads, dim] into the cache at positions start
+// .. start + tokens - 1 (kernels/attention.hip:480-493): a thread per chunk of
+// N values of a head, its key chunk one F16 store, its values N stores a
+// page apart (the value layout is transposed within a page).
+template <typename T>
+__global__ void __launch_bounds__(256) cache_write_chunks(const T* k, Extras<T> e, int64_t tokens, int kv_heads,
+                                                          int dim) {
+  constexpr int N = Chunk<T>::N;
+  const int per_head = dim / N;
+  const int64_t total = tokens * kv_heads * per_head;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const int c = (int)(i % per_head);
+    const int64_t row = i / per_head;  // token * kv_heads + head
+    int64_t key, value;
+    if (!cache_place(e, row / kv_heads, kv_heads, dim, (int)(row % kv_heads), key, value)) continue;
+    float kx[N], vx[N];
+    Chunk<T>::load(k + row * dim + c * N, kx);
+    Chunk<T>::load(e.v + row * dim + c * N, vx);
+    store_f16<N>(e.keys + key + c * N, kx);
+#pragma unroll
+    for (int j = 0; j < N; ++j) e.values[value + (int64_t)(c * N + j) * e.page_size] = (uint16_t)f16_bits(vx[j]);
+  }
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256) cache_write_values(const T* k, Extras<T> e, int64_t tokens, int kv_heads,
+                                                          int dim) {
+  const int64_t total = tokens * kv_heads * dim;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const int d = (int)(i % dim);
+    const int64_t row = i / dim;
+    int64_t key, value;
+    if (!cache_place(e, row / kv_heads, kv_heads, dim, (int)(row % kv_heads), key, value)) continue;
+    e.keys[key + d] = (uint16_t)f16_bits(load_one(k + i));
+    e.values[value + (int64_t)d * e.page_size] = (uint16_t)f16_bits(load_one(e.v + i));
+  }
+}
+
+// [rows, 2 d] into [rows, d] and [rows, d] (kernels/linear_attention.hip:
+// 298-307): a thread per 16-byte chunk of the outputs, or per value.
+template <typename T>
+__global__ void __launch_bounds__(256) split_halves_chunks(const T* x, T* first, T* second, int64_t rows, int d) {
+  constexpr int N = Chunk<T>::N;
+  const int per_row = d / N;
+  const int64_t total = rows * per_row;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const int64_t r = i / per_row;
+    const int c = (int)(i % per_row) * N;
+    const uint4 a = stream_load(x + r * 2 * d + c), b = stream_load(x + r * 2 * d + d + c);
+    __builtin_nontemporal_store(u32x4{a.x, a.y, a.z, a.w}, reinterpret_cast<u32x4*>(first + r * d + c));
+    __builtin_nontemporal_store(u32x4{b.x, b.y, b.z, b.w}, reinterpret_cast<u32x4*>(second + r * d + c));
+  }
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256) split_halves_values(const T* x, T* first, T* second, int64_t rows, int d) {
+  const int64_t total = rows * d;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const int64_t r = i / d;
+    const int c = (int)(i % d);
+    first[i] = x[r * 2 * d + c];
+    second[i] = x[r * 2 * d + d + c];
+  }
+}
+
+// ------------------------------------------------------------------ launch layer
+
+// Picks the kernel for a checked call: the per-lane-chunk one where heads
+// are whole 16-byte chunks with every value turning (and the tensors allow
+// 16-byte access), else the LDS one.
+template <typename T, bool EXTRAS>
+int qk_launch(const char* entry, const T* q, const T* k, T* q_out, T* k_out, const float* q_weight,
+              const float* k_weight, const int32_t* positions, const QkArgs& a, const Extras<T>& e, bool aligned,
+              hipStream_t st) {
+  const RopeArgs& p = a.rope;
+  constexpr int N = Chunk<T>::N;
+  const int dim = p.dim;
+  const int lanes_per_head = dim / (2 * N);
+  const bool whole = p.rotary == dim && dim % (2 * N) == 0 && (lanes_per_head & (lanes_per_head - 1)) == 0 &&
+                     lanes_per_head <= kWave / 2 && aligned;
+  if (!whole) {
+    hipLaunchKernelGGL((qk_norm_rope_kernel<T, EXTRAS>), dim3(grid_for(p.tokens, 1, 1 << 16)), dim3(256), 0, st, q,
+                       k, q_out, k_out, q_weight, k_weight, positions, a, e);
+    return launched(entry);
+  }
+  const int heads_per_wave = kWave / lanes_per_head;
+  // a wave per 64 / G heads, and a thread per weight of a head
+  const int waves = (int)std::min<int64_t>(
+      kQkMaxWaves, std::max<int64_t>(ceil_div(a.q_heads + a.kv_heads, heads_per_wave), ceil_div(dim, kWave)));
+  const dim3 grid(p.tokens), block(64 * waves);
+  switch (lanes_per_head) {
+#define DRIFT_QK_CASE(G)                                                                                             \
+  case G:                                                                                                            \
+    if (p.layout == DRIFT_ROPE_NEOX)                                                                                 \
+      hipLaunchKernelGGL((qk_norm_rope_token<T, G, true, EXTRAS>), grid, block, 0, st, q, k, q_out, k_out, q_weight, \
+                         k_weight, positions, a, e);                                                                 \
+    else                                                                                                             \
+      hipLaunchKernelGGL((qk_norm_rope_token<T, G, false, EXTRAS>), grid, block, 0, st, q, k, q_out, k_out,          \
+                         q_weight, k_weight, positions, a, e);                                                       \
+    break;
+    DRIFT_QK_CASE(1)
+    DRIFT_QK_CASE(2)
+    DRIFT_QK_CASE(4)
+    DRIFT_QK_CASE(8)
+    DRIFT_QK_CASE(16)
+    DRIFT_QK_CASE(32)
+#undef DRIFT_QK_CASE
+    default:
+      return refuse("%s: no kernel for heads of %d values", entry, dim);
+  }
+  return launched(entry);
+}
+
+template <typename T>
+int qk_norm_rope(const char* entry, const T* q, const T* k, T* q_out, T* k_out, const float* q_weight,
+                 const float* k_weight, const int32_t* positions, int32_t tokens, int32_t heads, int32_t kv_heads,
+                 int32_t dim, float eps, float offset, int32_t rotary, float theta, int32_t layout,
+                 int32_t sections, int32_t s0, int32_t s1, int32_t s2, int32_t s3, void* stream) {
+  clear_error();
+  const int32_t s[4] = {s0, s1, s2, s3};
+  if (kv_heads < 0) return refuse("%s: %d key heads", entry, kv_heads);
+  if (const int bad = check_rope(entry, tokens, heads, dim, rotary, layout, sections, s)) return bad;
+  if ((int64_t)tokens * (heads + kv_heads) == 0) return 0;
+  if (!positions || (heads > 0 && (!q || !q_out || !q_weight)) || (kv_heads > 0 && (!k || !k_out || !k_weight)))
+    return refuse("%s: null tensor", entry);
+  QkArgs a;
+  fill_rope(a.rope, tokens, heads, dim, rotary, theta, layout, sections, s);
+  a.q_heads = heads;
+  a.kv_heads = kv_heads;
+  a.eps = eps;
+  a.offset = offset;
+  a.q_stride = dim;
+  const bool aligned = (!q || (aligned16(q) && aligned16(q_out))) && (!k || (aligned16(k) && aligned16(k_out)));
+  return qk_launch<T, false>(entry, q, k, q_out, k_out, q_weight, k_weight, positions, a, Extras<T>{}, aligned,
+                             (hipStream_t)stream);
+}
+
+// attention_inputs: the checks of the reference's attentionInputs
+// (ops/HipAttention.scala:144-215: checkSplitHalves, checkRope,
+// checkCacheWrite and checkPageTable, ops/AttentionOps.scala:225-256), then
+// one launch.
+template <typename T>
+int attention_inputs(const char* entry, const T* query_and_gate, const T* k, const T* v, const float* q_norm,
+                     const float* k_norm, float eps, float offset, const int32_t* positions, int32_t tokens,
+                     int32_t heads, int32_t kv_heads, int32_t dim, int32_t rotary, float theta, int32_t layout,
+                     int32_t sections, int32_t s0, int32_t s1, int32_t s2, int32_t s3, T* queries, T* gate,
+                     uint16_t* keys, uint16_t* values, const int32_t* page_table, int32_t table_pages,
+                     int32_t cache_pages, int32_t page_size, int32_t start, int32_t* bad_page, void* stream) {
+  clear_error();
+  const int32_t s[4] = {s0, s1, s2, s3};
+  if (kv_heads < 0) return refuse("%s: %d key heads", entry, kv_heads);
+  if (const int bad = check_rope(entry, tokens, heads, dim, rotary, layout, sections, s)) return bad;
+  if (page_size <= 0 || page_size % 16 != 0) return refuse("%s: pages of %d tokens: not a multiple of 16", entry, page_size);
+  if (start < 0 || table_pages < 0 || cache_pages < 0)
+    return refuse("%s: start %d, %d table pages, %d cache pages", entry, start, table_pages, cache_pages);
+  if ((int64_t)table_pages * page_size < (int64_t)start + tokens)
+    return refuse("%s: a page table of %d pages for %lld positions", entry, table_pages,
+                  (long long)start + tokens);
+  if ((int64_t)tokens * (heads + kv_heads) == 0) return 0;
+  if (!positions || (heads > 0 && (!query_and_gate || !queries || !q_norm)) ||
+      (kv_heads > 0 && (!k || !v || !k_norm || !keys || !values || !page_table)))
+    return refuse("%s: null tensor", entry);
+  QkArgs a;
+  fill_rope(a.rope, tokens, heads, dim, rotary, theta, layout, sections, s);
+  a.q_heads = heads;
+  a.kv_heads = kv_heads;
+  a.eps = eps;
+  a.offset = offset;
+  a.q_stride = gate ? 2 * (int64_t)dim : dim;
+  const Extras<T> e{gate, v, keys, values, page_table, cache_pages, page_size, start, bad_page};
+  const bool aligned = (!query_and_gate || (aligned16(query_and_gate) && aligned16(queries))) &&
+                       (!gate || aligned16(gate)) && (!k || (aligned16(k) && aligned16(v))) &&
+                       (!keys || aligned16(keys));
+  return qk_launch<T, true>(entry, query_and_gate, k, queries, nullptr, q_norm, k_norm, positions, a, e, aligned,
+                            (hipStream_t)stream);
+}
+
+template <typename T>
+int cache_write(const char* entry, const T* k, const T* v, uint16_t* keys, uint16_t* values,
+                const int32_t* page_table, int32_t table_pages, int32_t cache_pages, int32_t tokens,
+                int32_t kv_heads, int32_t dim, int32_t page_size, int32_t start, int32_t* bad_page, void* stream) {
+  clear_error();
+  if (tokens < 0 || kv_heads < 0 || dim <= 0)
+    return refuse("%s: %d tokens of %d heads of %d values", entry, tokens, kv_heads, dim);
+  if (page_size <= 0 || page_size % 16 != 0) return refuse("%s: pages of %d tokens: not a multiple of 16", entry, page_size);
+  if (start < 0 || table_pages < 0 || cache_pages < 0)
+    return refuse("%s: start %d, %d table pages, %d cache pages", entry, start, table_pages, cache_pages);
+  if ((int64_t)table_pages * page_size < (int64_t)start + tokens)
+    return refuse("%s: a page table of %d pages for %lld positions", entry, table_pages,
+                  (long long)start + tokens);
+  if ((int64_t)tokens * kv_heads == 0) return 0;
+  if (!k || !v || !keys || !values || !page_table) return refuse("%s: null tensor", entry);
+  const Extras<T> e{nullptr, v, keys, values, page_table, cache_pages, page_size, start, bad_page};
+  constexpr int N = Chunk<T>::N;
+  const hipStream_t st = (hipStream_t)stream;
+  const int64_t values_count = (int64_t)tokens * kv_heads * dim;
+  if (dim % N == 0 && aligned16(k) && aligned16(v) && aligned16(keys))
+    hipLaunchKernelGGL(cache_write_chunks<T>, dim3(grid_for(values_count / N, 256, kOneShotBlocks)), dim3(256), 0, st,
+                       k, e, (int64_t)tokens, kv_heads, dim);
+  else
+    hipLaunchKernelGGL(cache_write_values<T>, dim3(grid_for(values_count, 256, kOneShotBlocks)), dim3(256), 0, st, k,
+                       e, (int64_t)tokens, kv_heads, dim);
+  return launched(entry);
+}
+
+template <typename T>
+int split_halves(const char* entry, const T* x, T* first, T* second, int64_t rows, int32_t d, void* stream) {
+  clear_error();
+  if (rows < 0 || d <= 0) return refuse("%s: %lld rows of 2 x %d values", entry, (long long)rows, d);
+  if (rows == 0) return 0;
+  if (!x || !first || !second) return refuse("%s: null tensor", entry);
+  constexpr int N = Chunk<T>::N;
+  const hipStream_t st = (hipStream_t)stream;
+  if (d % N == 0 && aligned16(x) && aligned16(first) && aligned16(second))
+    hipLaunchKernelGGL(split_halves_chunks<T>, dim3(grid_for(rows * (d / N), 256, kOneShotBlocks)), dim3(256), 0, st,
+                       x, first, second, rows, (int)d);
+  else
+    hipLaunchKernelGGL(split_halves_values<T>, dim3(grid_for(rows * d, 256, kOneShotBlocks)), dim3(256), 0, st, x,
+                       first, second, rows, (int)d);
+  return launched(entry);
+}
+
+}  // namespace
+}  // namespace drift
+
+using namespace drift;
+
+extern "C" int drift_qk_norm_rope_f32(const float* q, const float* k, float* q_out, float* k_out,
+                                      const float* q_weight, const float* k_weight, const int32_t* positions,
+                                      int32_t tokens, int32_t heads, int32_t kv_heads, int32_t head_dim, float eps,
+                                      float offset, int32_t rotary, float theta, int32_t layout, int32_t sections,
+                                      int32_t s0, int32_t s1, int32_t s2, int32_t s3, void* stream) {
+  return qk_norm_rope<float>("drift_qk_norm_rope_f32", q, k, q_out, k_out, q_weight, k_weight, positions, tokens,
+                             heads, kv_heads, head_dim, eps, offset, rotary, theta, layout, sections, s0, s1, s2, s3,
+                             stream);
+}
+
+extern "C" int drift_qk_norm_rope_bf16(const uint16_t* q, const uint16_t* k, uint16_t* q_out, uint16_t* k_out,
+                                       const float* q_weight, const float* k_weight, const int32_t* positions,
+                                       int32_t tokens, int32_t heads, int32_t kv_heads, int32_t head_dim, float eps,
+                                       float offset, int32_t rotary, float theta, int32_t layout, int32_t sections,
+                                       int32_t s0, int32_t s1, int32_t s2, int32_t s3, void* stream) {
+  return qk_norm_rope<uint16_t>("drift_qk_norm_rope_bf16", q, k, q_out, k_out, q_weight, k_weight, positions, tokens,
+                                heads, kv_heads, head_dim, eps, offset, rotary, theta, layout, sections, s0, s1, s2,
+                                s3, stream);
+}
+
+extern "C" int drift_attention_inputs_f32(const float* query_and_gate, const float* k, const float* v,
+                                          const float* q_norm, const float* k_norm, float eps, float offset,
+                                          const int32_t* positions, int32_t tokens, int32_t heads, int32_t kv_heads,
+                                          int32_t head_dim, int32_t rotary, float theta, int32_t layout,
+                                          int32_t sections, int32_t s0, int32_t s1, int32_t s2, int32_t s3,
+                                          float* queries, float* gate, uint16_t* keys, uint16_t* values,
+                                          const int32_t* page_table, int32_t table_pages, int32_t cache_pages,
+                                          int32_t page_size, int32_t start, int32_t* bad_page, void* stream) {
+  return attention_inputs<float>("drift_attention_inputs_f32", query_and_gate, k, v, q_norm, k_norm, eps, offset,
+                                 positions, tokens, heads, kv_heads, head_dim, rotary, theta, layout, sections, s0,
+                                 s1, s2, s3, queries, gate, keys, values, page_table, table_pages, cache_pages,
+                                 page_size, start, bad_page, stream);
+}
+
+extern "C" int drift_attention_inputs_bf16(const uint16_t* query_and_gate, const uint16_t* k, const uint16_t* v,
+                                           const float* q_norm, const float* k_norm, float eps, float offset,
+                                           const int32_t* positions, int32_t tokens, int32_t heads, int32_t kv_heads,
+                                           int32_t head_dim, int32_t rotary, float theta, int32_t layout,
+                                           int32_t sections, int32_t s0, int32_t s1, int32_t s2, int32_t s3,
+                                           uint16_t* queries, uint16_t* gate, uint16_t* keys, uint16_t* values,
+                                           const int32_t* page_table, int32_t table_pages, int32_t cache_pages,
+                                           int32_t page_size, int32_t start, int32_t* bad_page, void* stream) {
+  return attention_inputs<uint16_t>("drift_attention_inputs_bf16", query_and_gate, k, v, q_norm, k_norm, eps,
+                                    offset, positions, tokens, heads, kv_heads, head_dim, rotary, theta, layout,
+                                    sections, s0, s1, s2, s3, queries, gate, keys, values, page_table, table_pages,
+                                    cache_pages, page_size, start, bad_page, stream);
+}
+
+extern "C" int drift_cache_write_f32(const float* k, const float* v, uint16_t* keys, uint16_t* values,
+                                     const int32_t* page_table, int32_t table_pages, int32_t cache_pages,
+                                     int32_t tokens, int32_t kv_heads, int32_t head_dim, int32_t page_size,
+                                     int32_t start, int32_t* bad_page, void* stream) {
+  return cache_write<float>("drift_cache_write_f32", k, v, keys, values, page_table, table_pages, cache_pages, tokens,
+                            kv_heads, head_dim, page_size, start, bad_page, stream);
+}
+
+extern "C" int drift_cache_write_bf16(const uint16_t* k, const uint16_t* v, uint16_t* keys, uint16_t* values,
+                                      const int32_t* page_table, int32_t table_pages, int32_t cache_pages,
+                                      int32_t tokens, int32_t kv_heads, int32_t head_dim, int32_t page_size,
+                                      int32_t start, int32_t* bad_page, void* stream) {
+  return cache_write<uint16_t>("drift_cache_write_bf16", k, v, keys, values, page_table, table_pages, cache_pages,
+                               tokens, kv_heads, head_dim, page_size, start, bad_page, stream);
+}
+
+extern "C" int drift_split_halves_f32(const float* x, float* first, float* second, int64_t rows, int32_t d,
+                                      void* stream) {
+  return split_halves<float>("drift_split_halves_f32", x, first, second, rows, d, stream);
+}
+
+extern "C" int drift_split_halves_bf16(const uint16_t* x, uint16_t* first, uint16_t* second, int64_t rows, int32_t d,
+                                       void* stream) {
+  return split_halves<uint16_t>("drift_split_halves_bf16", x, first, second, rows, d, stream);
+}

@@ -16,85 +16,13 @@
 // of it in double, the turn a*c - b*s, a*s + b*c in double, rounded once.
 // Wan's tables (models/Wan.scala:324-361) are cos and sin of a double angle
 // rounded to float; rope_3d makes exactly those values.
-#include "common.hpp"
+#include "rope.hpp"
 
 #include <algorithm>
 #include <climits>
 
 namespace drift {
 namespace {
-
-constexpr int kMaxPairs = 256;  // head_dim up to 512
-
-struct RopeArgs {
-  float inverse[kMaxPairs];  // per pair, as the CPU computes it
-  int32_t tokens, heads, dim, rotary, layout, sections;
-  int32_t s[4];
-};
-
-__device__ __forceinline__ int rope_section(int pair, const RopeArgs& p) {
-  switch (p.sections) {
-    case DRIFT_SECTIONS_CONTIGUOUS:
-      return pair < p.s[0] ? 0 : (pair < p.s[0] + p.s[1] ? 1 : 2);
-    case DRIFT_SECTIONS_INTERLEAVED:
-      if (pair % 3 == 1 && pair < 3 * p.s[1]) return 1;
-      if (pair % 3 == 2 && pair < 3 * p.s[2]) return 2;
-      return 0;
-    case DRIFT_SECTIONS_AXES:
-      return pair < p.s[0] ? 0 : (pair < p.s[0] + p.s[1] ? 1 : (pair < p.s[0] + p.s[1] + p.s[2] ? 2 : 3));
-    default:
-      return 0;
-  }
-}
-
-// The token's cos and sin for every pair, into cs (LDS), by the block.
-__device__ __forceinline__ void token_angles(const RopeArgs& p, const int32_t* positions, int64_t t, double2* cs) {
-  const int half = p.rotary / 2;
-  for (int j = threadIdx.x; j < half; j += blockDim.x) {
-    const int32_t position = positions[(int64_t)rope_section(j, p) * p.tokens + t];
-    const float angle = (float)position * p.inverse[j];
-    double sn, cn;
-    sincos((double)angle, &sn, &cn);
-    cs[j] = make_double2(cn, sn);
-  }
-}
-
-// The turn of one pair (a first, b second) in double, as the CPU does it.
-__device__ __forceinline__ void turn(double a, double b, double c, double s, float& first, float& second) {
-  first = (float)(a * c - b * s);
-  second = (float)(a * s + b * c);
-}
-
-// The same turn with one rounding per output: a*c - b*s as fma(a, c, -(b*s)).
-// It differs from the two-rounding form only when the double result lies
-// within a double ulp of a float rounding boundary (about 2^-28 of values).
-__device__ __forceinline__ void turn_fused(double a, double b, double c, double s, float& first, float& second) {
-  first = (float)fma(a, c, -(b * s));
-  second = (float)fma(a, s, b * c);
-}
-
-// Pair slot j of one head (slots cover the head: j < rotary/2 turn a pair,
-// the rest copy two tail values), scalar loads. Reads before it writes.
-template <typename T, typename Load>
-__device__ __forceinline__ void turn_slot(int j, int dim, int rotary, int layout, const double2* cs, Load load,
-                                          T* head_out) {
-  const int half = rotary / 2;
-  if (j < half) {
-    const int d0 = layout == DRIFT_ROPE_NEOX ? j : 2 * j;
-    const int d1 = layout == DRIFT_ROPE_NEOX ? j + half : 2 * j + 1;
-    const double a = load(d0), b = load(d1);
-    float f, s;
-    turn(a, b, cs[j].x, cs[j].y, f, s);
-    store_one(head_out + d0, f);
-    store_one(head_out + d1, s);
-  } else {
-    const int e = rotary + 2 * (j - half);
-    const float v0 = load(e);
-    const float v1 = e + 1 < dim ? (float)load(e + 1) : 0.0f;
-    store_one(head_out + e, v0);
-    if (e + 1 < dim) store_one(head_out + e + 1, v1);
-  }
-}
 
 // ------------------------------------------------------------------ rope
 
@@ -324,233 +252,7 @@ __global__ void __launch_bounds__(kRope3dWaves * 64) rope_3d_waves(const T* x, T
   }
 }
 
-// ------------------------------------------------------------------ per-head RMSNorm + rope
-
-struct QkArgs {
-  RopeArgs rope;
-  int32_t q_heads, kv_heads;
-  float eps, offset;
-};
-
-// Any head size: each wave norms one head row at a time into LDS (the F32
-// values rmsNorm writes), then turns its pairs from there.
-template <typename T>
-__global__ void __launch_bounds__(256) qk_norm_rope_kernel(const T* q, const T* k, T* q_out, T* k_out,
-                                                           const float* q_weight, const float* k_weight,
-                                                           const int32_t* positions, QkArgs a) {
-  __shared__ double2 cs[kMaxPairs];
-  __shared__ float normed[4][2 * kMaxPairs];
-  const RopeArgs& p = a.rope;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int rows = a.q_heads + a.kv_heads;
-  const int slots = (p.dim + 1) / 2;
-  for (int64_t t = blockIdx.x; t < p.tokens; t += gridDim.x) {
-    token_angles(p, positions, t, cs);
-    for (int round = 0; round < rows; round += 4) {
-      const int h = round + wave;
-      const bool query = h < a.q_heads;
-      const T* xh = query ? q + (t * a.q_heads + h) * p.dim : k + (t * a.kv_heads + (h - a.q_heads)) * p.dim;
-      T* oh = query ? q_out + (t * a.q_heads + h) * p.dim : k_out + (t * a.kv_heads + (h - a.q_heads)) * p.dim;
-      const float* w = query ? q_weight : k_weight;
-      if (h < rows) {
-        float v[2 * kMaxPairs / kWave];
-        double squares = 0.0;
-#pragma unroll
-        for (int i = 0; i < 2 * kMaxPairs / kWave; ++i) {
-          const int d = i * kWave + lane;
-          v[i] = d < p.dim ? load_one(xh + d) : 0.0f;
-          squares = fma((double)v[i], (double)v[i], squares);
-        }
-        const double factor = 1.0 / sqrt(group_sum<64>(squares) / (double)p.dim + (double)a.eps);
-#pragma unroll
-        for (int i = 0; i < 2 * kMaxPairs / kWave; ++i) {
-          const int d = i * kWave + lane;
-          if (d < p.dim) normed[wave][d] = (float)((double)v[i] * factor * ((double)w[d] + (double)a.offset));
-        }
-      }
-      __syncthreads();  // normed rows and (first round) cs are ready
-      if (h < rows)
-        for (int j = lane; j < slots; j += kWave)
-          turn_slot<T>(j, p.dim, p.rotary, p.layout, cs, [&](int d) { return (double)normed[wave][d]; }, oh);
-      __syncthreads();  // normed is reused next round, cs next token
-    }
-  }
-}
-
-// The fast path for whole-chunk heads with every value turning: one block per
-// token, G lanes per head, each lane holding two chunks of its head (NeoX: a
-// chunk and its partner; otherwise chunks i and i + G), 64 / G heads per
-// wave. The grid covers the tokens in one pass. Each lane issues its loads
-// first; while they land the block makes the token's cos and sin (one sincos
-// per pair) and the norm weights (+ offset, in double) into LDS.
-//
-// LDS is laid out so the G lanes of a head read consecutive entries: for NeoX
-// the pair (and weight) of lane i0's value i sits at i * G + i0 (the natural
-// index would put the G lanes N entries apart, on the same banks).
-template <bool NEOX, int G, int N>
-__device__ __forceinline__ int qk_pair_slot(int pair) {
-  if constexpr (NEOX) return (pair % N) * G + pair / N;
-  return pair;
-}
-
-template <bool NEOX, int G, int N>
-__device__ __forceinline__ int qk_weight_slot(int d) {
-  if constexpr (NEOX) {
-    const int half = N * G;
-    const int h = d >= half ? 1 : 0, e = d - h * half;
-    return h * half + (e % N) * G + e / N;
-  }
-  return d;
-}
-
-constexpr int kQkMaxWaves = 16;
-
-template <typename T, int G, bool NEOX>
-__global__ void __launch_bounds__(kQkMaxWaves * 64) qk_norm_rope_token(const T* q, const T* k, T* q_out, T* k_out,
-                                                                     const float* q_weight, const float* k_weight,
-                                                                     const int32_t* positions, QkArgs a) {
-  constexpr int N = Chunk<T>::N;
-  using Raw = typename Chunk<T>::Raw;
-  constexpr int kHeadsPerWave = kWave / G;
-  constexpr int kPairs = N * G;  // a head's pairs (rotary == dim == 2 N G)
-  __shared__ double2 cs[kPairs];
-  __shared__ double weights[2][2 * kPairs];
-  const RopeArgs& p = a.rope;
-  constexpr int dim = 2 * N * G, half = N * G;
-  const int64_t t = blockIdx.x;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int waves = blockDim.x >> 6;
-  const int rows = a.q_heads + a.kv_heads;
-  const int i0 = lane % G;
-  const int d0 = i0 * N, d1 = (NEOX ? half : G * N) + i0 * N;
-  auto head_at = [&](auto* qs, auto* ks, int h) {
-    return h < a.q_heads ? qs + (t * a.q_heads + h) * dim : ks + (t * a.kv_heads + (h - a.q_heads)) * dim;
-  };
-  // the angles' and weights' operands load first: a wave's loads complete in
-  // issue order, so the tables are made while the heads are still loading
-  const int j = threadIdx.x, jp = min(j, half - 1), jd = min(j, dim - 1);
-  const int32_t position = positions[(int64_t)rope_section(jp, p) * p.tokens + t];
-  const float inverse = p.inverse[jp];
-  const float qw = q_weight[jd], kw = k_weight[jd];
-  // loads are never branched around (the wait for the angles' operands would
-  // then wait for them too): a head past the last is clamped to it
-  int h = wave * kHeadsPerWave + lane / G;
-  const T* xh = head_at(q, k, min(h, rows - 1));
-  Raw r0 = Chunk<T>::load_raw(xh + d0);
-  Raw r1 = Chunk<T>::load_raw(xh + d1);
-  if (j < half) {
-    double sn, cn;
-    sincos((double)((float)position * inverse), &sn, &cn);
-    cs[qk_pair_slot<NEOX, G, N>(j)] = make_double2(cn, sn);
-  }
-  if (j < dim) {
-    const int slot = qk_weight_slot<NEOX, G, N>(j);
-    weights[0][slot] = (double)qw + (double)a.offset;
-    weights[1][slot] = (double)kw + (double)a.offset;
-  }
-  __syncthreads();
-  for (;;) {
-    const bool live = h < rows;
-    float v0[N], v1[N];
-    double squares = 0.0;
-    if (live) {
-      Chunk<T>::unpack(r0, v0);
-      Chunk<T>::unpack(r1, v1);
-#pragma unroll
-      for (int i = 0; i < N; ++i) {
-        squares = fma((double)v0[i], (double)v0[i], squares);
-        squares = fma((double)v1[i], (double)v1[i], squares);
-      }
-    }
-    squares = group_sum<G>(squares);
-    if (live) {
-      const double factor = 1.0 / sqrt(squares / (double)dim + (double)a.eps);
-      const double* w = weights[h < a.q_heads ? 0 : 1];
-#pragma unroll
-      for (int i = 0; i < N; ++i) {
-        v0[i] = (float)((double)v0[i] * factor * w[qk_weight_slot<NEOX, G, N>(d0 + i)]);
-        v1[i] = (float)((double)v1[i] * factor * w[qk_weight_slot<NEOX, G, N>(d1 + i)]);
-      }
-      if constexpr (NEOX) {
-#pragma unroll
-        for (int i = 0; i < N; ++i) {
-          const double2 c = cs[qk_pair_slot<NEOX, G, N>(d0 + i)];
-          turn_fused(v0[i], v1[i], c.x, c.y, v0[i], v1[i]);
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < N; i += 2) {
-          const double2 c0 = cs[(d0 + i) / 2], c1 = cs[(d1 + i) / 2];
-          turn_fused(v0[i], v0[i + 1], c0.x, c0.y, v0[i], v0[i + 1]);
-          turn_fused(v1[i], v1[i + 1], c1.x, c1.y, v1[i], v1[i + 1]);
-        }
-      }
-      T* oh = head_at(q_out, k_out, h);
-      Chunk<T>::store(oh + d0, v0);
-      Chunk<T>::store(oh + d1, v1);
-    }
-    // more heads than the block has waves for: the next pass of this wave
-    h += waves * kHeadsPerWave;
-    if (h - lane / G >= rows) break;
-    xh = head_at(q, k, min(h, rows - 1));
-    r0 = Chunk<T>::load_raw(xh + d0);
-    r1 = Chunk<T>::load_raw(xh + d1);
-  }
-}
-
 // ------------------------------------------------------------------ launch layer
-
-int check_rope(const char* entry, int32_t tokens, int32_t heads, int32_t dim, int32_t rotary, int32_t layout,
-               int32_t sections, const int32_t (&s)[4]) {
-  if (tokens < 0 || heads < 0) return refuse("%s: %d tokens of %d heads", entry, tokens, heads);
-  if (dim <= 0 || dim > 2 * kMaxPairs) return refuse("%s: heads of %d values (at most %d)", entry, dim, 2 * kMaxPairs);
-  if (rotary < 0 || rotary % 2 != 0 || rotary > dim)
-    return refuse("%s: %d rotary dimensions in heads of %d", entry, rotary, dim);
-  if (layout != DRIFT_ROPE_NEOX && layout != DRIFT_ROPE_INTERLEAVED) return refuse("%s: no layout %d", entry, layout);
-  if (sections < DRIFT_SECTIONS_SINGLE || sections > DRIFT_SECTIONS_AXES)
-    return refuse("%s: no sections %d", entry, sections);
-  if (sections == DRIFT_SECTIONS_AXES) {
-    int count = 0, sum = 0;
-    for (int a = 0; a < 4; ++a) {
-      if (s[a] < 0 || (s[a] == 0 && a + 1 < 4 && s[a + 1] > 0))
-        return refuse("%s: axes of %d %d %d %d pairs", entry, s[0], s[1], s[2], s[3]);
-      count += s[a] > 0;
-      sum += s[a];
-    }
-    if (count == 0 || 2 * sum != rotary)
-      return refuse("%s: axes of %d %d %d %d pairs for %d rotary values", entry, s[0], s[1], s[2], s[3], rotary);
-  }
-  if ((sections == DRIFT_SECTIONS_CONTIGUOUS || sections == DRIFT_SECTIONS_INTERLEAVED) &&
-      (s[0] < 0 || s[1] < 0 || s[2] < 0))
-    return refuse("%s: sections %d %d %d", entry, s[0], s[1], s[2]);
-  return 0;
-}
-
-// The inverse frequencies as the CPU reference makes them
-// (ops/CpuAttention.scala:124-133).
-void fill_rope(RopeArgs& p, int32_t tokens, int32_t heads, int32_t dim, int32_t rotary, float theta, int32_t layout,
-               int32_t sections, const int32_t (&s)[4]) {
-  p.tokens = tokens;
-  p.heads = heads;
-  p.dim = dim;
-  p.rotary = rotary;
-  p.layout = layout;
-  p.sections = sections;
-  for (int a = 0; a < 4; ++a) p.s[a] = s[a];
-  for (int pair = 0; pair < kMaxPairs; ++pair) {
-    if (pair >= rotary / 2) {
-      p.inverse[pair] = 0.0f;
-      continue;
-    }
-    double exponent = 2.0 * pair / (double)rotary;
-    if (sections == DRIFT_SECTIONS_AXES) {
-      int start = 0, axis = 0;
-      while (pair >= start + s[axis]) start += s[axis++];
-      exponent = (double)(pair - start) / (double)s[axis];
-    }
-    p.inverse[pair] = 1.0f / (float)std::pow((double)theta, exponent);
-  }
-}
 
 template <typename T>
 int rope(const char* entry, const T* x, const int32_t* positions, T* out, int32_t tokens, int32_t heads,
@@ -657,64 +359,6 @@ int rope_3d(const char* entry, const T* x, T* out, int64_t tokens, int32_t heads
   return launched(entry);
 }
 
-template <typename T>
-int qk_norm_rope(const char* entry, const T* q, const T* k, T* q_out, T* k_out, const float* q_weight,
-                 const float* k_weight, const int32_t* positions, int32_t tokens, int32_t heads, int32_t kv_heads,
-                 int32_t dim, float eps, float offset, int32_t rotary, float theta, int32_t layout,
-                 int32_t sections, int32_t s0, int32_t s1, int32_t s2, int32_t s3, void* stream) {
-  clear_error();
-  const int32_t s[4] = {s0, s1, s2, s3};
-  if (kv_heads < 0) return refuse("%s: %d key heads", entry, kv_heads);
-  if (const int bad = check_rope(entry, tokens, heads, dim, rotary, layout, sections, s)) return bad;
-  if ((int64_t)tokens * (heads + kv_heads) == 0) return 0;
-  if (!positions || (heads > 0 && (!q || !q_out || !q_weight)) || (kv_heads > 0 && (!k || !k_out || !k_weight)))
-    return refuse("%s: null tensor", entry);
-  QkArgs a;
-  fill_rope(a.rope, tokens, heads, dim, rotary, theta, layout, sections, s);
-  a.q_heads = heads;
-  a.kv_heads = kv_heads;
-  a.eps = eps;
-  a.offset = offset;
-  constexpr int N = Chunk<T>::N;
-  const int lanes_per_head = dim / (2 * N);
-  const bool whole = rotary == dim && dim % (2 * N) == 0 && (lanes_per_head & (lanes_per_head - 1)) == 0 &&
-                     lanes_per_head <= kWave / 2 && (!q || (aligned16(q) && aligned16(q_out))) &&
-                     (!k || (aligned16(k) && aligned16(k_out)));
-  const dim3 grid(grid_for(tokens, 1, 1 << 16));
-  const hipStream_t st = (hipStream_t)stream;
-  if (whole) {
-    const int heads_per_wave = kWave / lanes_per_head;
-    // a wave per 64 / G heads, and a thread per weight of a head
-    const int waves = (int)std::min<int64_t>(
-        kQkMaxWaves, std::max<int64_t>(ceil_div(heads + kv_heads, heads_per_wave), ceil_div(dim, kWave)));
-    const dim3 block(64 * waves);
-    switch (lanes_per_head) {
-#define DRIFT_QK_CASE(G)                                                                                         \
-  case G:                                                                                                        \
-    if (layout == DRIFT_ROPE_NEOX)                                                                               \
-      hipLaunchKernelGGL((qk_norm_rope_token<T, G, true>), dim3(tokens), block, 0, st, q, k, q_out, k_out,       \
-                         q_weight, k_weight, positions, a);                                                      \
-    else                                                                                                         \
-      hipLaunchKernelGGL((qk_norm_rope_token<T, G, false>), dim3(tokens), block, 0, st, q, k, q_out, k_out,      \
-                         q_weight, k_weight, positions, a);                                                      \
-    break;
-      DRIFT_QK_CASE(1)
-      DRIFT_QK_CASE(2)
-      DRIFT_QK_CASE(4)
-      DRIFT_QK_CASE(8)
-      DRIFT_QK_CASE(16)
-      DRIFT_QK_CASE(32)
-#undef DRIFT_QK_CASE
-      default:
-        return refuse("%s: no kernel for heads of %d values", entry, dim);
-    }
-  } else {
-    hipLaunchKernelGGL(qk_norm_rope_kernel<T>, grid, dim3(256), 0, st, q, k, q_out, k_out, q_weight, k_weight,
-                       positions, a);
-  }
-  return launched(entry);
-}
-
 }  // namespace
 }  // namespace drift
 
@@ -760,24 +404,4 @@ extern "C" int drift_rope_3d_bf16(const uint16_t* x, uint16_t* out, int64_t toke
                                   int64_t token_offset, double theta, void* stream) {
   return rope_3d<uint16_t>("drift_rope_3d_bf16", x, out, tokens, heads, head_dim, frames, grid_rows, grid_cols,
                            token_offset, theta, stream);
-}
-
-extern "C" int drift_qk_norm_rope_f32(const float* q, const float* k, float* q_out, float* k_out,
-                                      const float* q_weight, const float* k_weight, const int32_t* positions,
-                                      int32_t tokens, int32_t heads, int32_t kv_heads, int32_t head_dim, float eps,
-                                      float offset, int32_t rotary, float theta, int32_t layout, int32_t sections,
-                                      int32_t s0, int32_t s1, int32_t s2, int32_t s3, void* stream) {
-  return qk_norm_rope<float>("drift_qk_norm_rope_f32", q, k, q_out, k_out, q_weight, k_weight, positions, tokens,
-                             heads, kv_heads, head_dim, eps, offset, rotary, theta, layout, sections, s0, s1, s2, s3,
-                             stream);
-}
-
-extern "C" int drift_qk_norm_rope_bf16(const uint16_t* q, const uint16_t* k, uint16_t* q_out, uint16_t* k_out,
-                                       const float* q_weight, const float* k_weight, const int32_t* positions,
-                                       int32_t tokens, int32_t heads, int32_t kv_heads, int32_t head_dim, float eps,
-                                       float offset, int32_t rotary, float theta, int32_t layout, int32_t sections,
-                                       int32_t s0, int32_t s1, int32_t s2, int32_t s3, void* stream) {
-  return qk_norm_rope<uint16_t>("drift_qk_norm_rope_bf16", q, k, q_out, k_out, q_weight, k_weight, positions, tokens,
-                                heads, kv_heads, head_dim, eps, offset, rotary, theta, layout, sections, s0, s1, s2,
-                                s3, stream);
 }

@@ -106,6 +106,30 @@ class QueryKeyNorms:
 
 
 @dataclass
+class KvCache:
+    """ops/KvCache.scala:5-22: a paged cache of pages of `pageSize` tokens;
+    keys F16 [pages, pageSize, kvHeads, headDimension], values F16 [pages,
+    kvHeads, headDimension, pageSize] (transposed within a page)."""
+    keys: torch.Tensor
+    values: torch.Tensor
+    pageSize: int
+
+    def __post_init__(self):
+        _require(self.pageSize % 16 == 0, f"pages of {self.pageSize} tokens: not a multiple of 16")
+        _require(self.keys.dtype == F16 and self.values.dtype == F16, "the cache is F16")
+        _require(self.keys.dim() == 4 and self.values.dim() == 4, "the cache's keys and values are 4-dimensional")
+        self.pages, _, self.kvHeads, self.headDimension = (int(d) for d in self.keys.shape)
+        _require(tuple(self.values.shape) == (self.pages, self.kvHeads, self.headDimension, self.pageSize),
+                 f"cache values {_shape(self.values)} for keys {_shape(self.keys)}")
+
+    @staticmethod
+    def allocate(pages: int, pageSize: int, kvHeads: int, headDimension: int, device="cuda") -> "KvCache":
+        """HipOps.allocateCache: the cache's two tensors, uninitialised."""
+        return KvCache(torch.empty((pages, pageSize, kvHeads, headDimension), dtype=F16, device=device),
+                       torch.empty((pages, kvHeads, headDimension, pageSize), dtype=F16, device=device), pageSize)
+
+
+@dataclass
 class Q8_0Table:
     """A Q8_0 table ([vocabulary, cols] values) as its bytes: a uint8 tensor
     [vocabulary, cols / 32 * 34], per 32 values an fp16 scale then 32 int8
@@ -257,6 +281,33 @@ def checkEmbedding(table, ids, out) -> None:
     _require(out.dtype in _FLOAT_TYPES, f"embedding takes F32 or BF16, not {_name(out.dtype)}")
     _require(tuple(out.shape) == (ids.shape[0], shape[-1]),
              f"embedding: out {_shape(out)} for {ids.shape[0]} rows of {shape[-1]}")
+
+
+def checkPageTable(pageTable, cache: KvCache, positions: int) -> None:
+    """ops/AttentionOps.scala:243-256."""
+    _require(pageTable.dtype == I32 and pageTable.dim() == 1,
+             f"a page table is I32 [pages], not {_name(pageTable.dtype)} {_shape(pageTable)}")
+    _require(pageTable.numel() * cache.pageSize >= positions,
+             f"a page table of {pageTable.numel()} pages for {positions} positions")
+
+
+def checkCacheWrite(k, v, cache: KvCache, pageTable, start: int) -> int:
+    """ops/AttentionOps.scala:225-241; returns the token count."""
+    checkElementwise("cacheWrite", k, v)
+    _require(k.dim() == 3 and tuple(k.shape[1:]) == (cache.kvHeads, cache.headDimension),
+             f"cacheWrite: {_shape(k)} into a cache of {cache.kvHeads} heads of {cache.headDimension}")
+    tokens = int(k.shape[0])
+    checkPageTable(pageTable, cache, start + tokens)
+    return tokens
+
+
+def checkSplitHalves(x, first, second) -> None:
+    """ops/LayoutOps.scala:73-80 (F32, or BF16 here)."""
+    checkElementwise("splitHalves", x)
+    checkElementwise("splitHalves", first, second)
+    _require(x.dtype == first.dtype, f"splitHalves takes one type, not {_name(x.dtype)} and {_name(first.dtype)}")
+    _require(x.numel() == 2 * first.numel() and first.dim() >= 1 and x.shape[-1] == 2 * first.shape[-1],
+             f"splitHalves: {_shape(x)} into {_shape(first)}")
 
 
 _CONVERSIONS = {(F32, BF16): 0, (BF16, F32): 1, (F32, F16): 2, (F16, F32): 3}
@@ -566,6 +617,86 @@ class HipOps:
                      _ptr(rotatedKeys), _ptr(norms.queryNorm), _ptr(norms.keyNorm), _ptr(positions), tokens, heads,
                      kv, d, norms.epsilon, norms.weightOffset, r.rotaryDimensions, r.theta, int(r.layout),
                      r.sections.code, *r.sections.launch_sizes())
+
+    # ---------------------------------------------------------------- attention inputs
+
+    # attention.hip's ATTENTION_INPUT_DIMENSION (ops/HipAttention.scala:217-218)
+    AttentionInputDimension = 512
+
+    def cacheWrite(self, k, v, cache: KvCache, pageTable, start: int, badPage: Optional[torch.Tensor] = None) -> None:
+        """Keys and values [tokens, kvHeads, D] into the cache at positions
+        start .. start + tokens - 1 (ops/AttentionOps.scala:52-63). A page
+        table entry outside the cache (which the reference fails on) writes
+        nothing and sets `badPage` (int32 [1], device) to 1 when given."""
+        tokens = checkCacheWrite(k, v, cache, pageTable, start)
+        _on_device("cacheWrite", k, v, cache.keys, cache.values, pageTable)
+        self._launch(f"drift_cache_write_{_suffix(k.dtype)}", _ptr(k), _ptr(v), _ptr(cache.keys), _ptr(cache.values),
+                     _ptr(pageTable), pageTable.numel(), cache.pages, tokens, cache.kvHeads, cache.headDimension,
+                     cache.pageSize, start, _ptr(badPage))
+
+    def splitHalves(self, x, first, second) -> None:
+        """Rows [.., 2 d] into their halves (ops/LayoutOps.scala:31)."""
+        checkSplitHalves(x, first, second)
+        _on_device("splitHalves", x, first, second)
+        d = first.shape[-1]
+        self._launch(f"drift_split_halves_{_suffix(x.dtype)}", _ptr(x), _ptr(first), _ptr(second), first.numel() // d,
+                     d)
+
+    def attentionInputs(self, queryAndGate, keys, values, norms: QueryKeyNorms, positions, cache: KvCache, pageTable,
+                        start: int, queries, gate, rotatedKeys, rotatedQueries,
+                        badPage: Optional[torch.Tensor] = None) -> None:
+        """A gated attention's inputs in one launch (ops/AttentionOps.scala:
+        66-107, ops/HipAttention.scala:144-215): the query halves of
+        `queryAndGate` [t, heads, 2 D] normed and turned into
+        `rotatedQueries`, the gate halves into `gate`, the keys normed,
+        turned and written to `cache` with `values` at `start`. `queries` and
+        `rotatedKeys` are the unfused steps' scratch, checked and not written,
+        as the reference's fused launch leaves them."""
+        t, heads, d = (int(n) for n in queries.shape) if queries.dim() == 3 else (0, 0, 0)
+        _require(d <= self.AttentionInputDimension,
+                 f"attentionInputs: heads of {d} values (at most {self.AttentionInputDimension} fused)")
+        checkSplitHalves(queryAndGate, queries, gate)
+        checkRope(queries, positions, norms.rope, rotatedQueries)
+        checkRope(keys, positions, norms.rope, rotatedKeys)
+        checkCacheWrite(rotatedKeys, values, cache, pageTable, start)
+        self._attentionInputs(queryAndGate, keys, values, norms, positions, cache, pageTable, start, gate,
+                              rotatedQueries, badPage)
+
+    def queryKeyNormRopeCache(self, q, k, v, norms: QueryKeyNorms, positions, cache: KvCache, pageTable, start: int,
+                              rotatedQueries, badPage: Optional[torch.Tensor] = None) -> None:
+        """The dense decoders' attention inputs in one launch: per-head RMS
+        norms of q [t, heads, D] and k [t, kvHeads, D], their rope, the
+        queries into `rotatedQueries` and the keys, with the values v, into
+        the cache at `start` (models/DenseDecoder.scala:834-863 runs rmsNorm,
+        rmsNorm, rope, rope, cacheWrite)."""
+        _require(q.dim() == 3 and q.shape[2] <= self.AttentionInputDimension,
+                 f"queryKeyNormRopeCache: queries {_shape(q)}")
+        checkRope(q, positions, norms.rope, rotatedQueries)
+        checkRope(k, positions, norms.rope, k)
+        checkCacheWrite(k, v, cache, pageTable, start)
+        self._attentionInputs(q, k, v, norms, positions, cache, pageTable, start, None, rotatedQueries, badPage)
+
+    def _attentionInputs(self, queryAndGate, keys, values, norms, positions, cache, pageTable, start, gate,
+                         rotatedQueries, badPage) -> None:
+        tokens, heads, d = (int(n) for n in rotatedQueries.shape)
+        _require(tuple(keys.shape) == (tokens, cache.kvHeads, d),
+                 f"attentionInputs: keys {_shape(keys)} for {tokens} tokens of heads of {d}")
+        _require(queryAndGate.dtype == keys.dtype == values.dtype == rotatedQueries.dtype and
+                 (gate is None or gate.dtype == keys.dtype),
+                 "attentionInputs takes one type for queries, gate, keys and values")
+        for name, w in (("queryNorm", norms.queryNorm), ("keyNorm", norms.keyNorm)):
+            requireF32("attentionInputs", w)
+            _require(tuple(w.shape) == (d,), f"attentionInputs: {name} {_shape(w)} for heads of {d}")
+        tensors = [queryAndGate, keys, values, norms.queryNorm, norms.keyNorm, positions, cache.keys, cache.values,
+                   pageTable, rotatedQueries] + ([] if gate is None else [gate])
+        _on_device("attentionInputs", *tensors)
+        r = norms.rope
+        self._launch(f"drift_attention_inputs_{_suffix(keys.dtype)}", _ptr(queryAndGate), _ptr(keys), _ptr(values),
+                     _ptr(norms.queryNorm), _ptr(norms.keyNorm), norms.epsilon, norms.weightOffset, _ptr(positions),
+                     tokens, heads, cache.kvHeads, d, r.rotaryDimensions, r.theta, int(r.layout), r.sections.code,
+                     *r.sections.launch_sizes(), _ptr(rotatedQueries), _ptr(gate), _ptr(cache.keys),
+                     _ptr(cache.values), _ptr(pageTable), pageTable.numel(), cache.pages, cache.pageSize, start,
+                     _ptr(badPage))
 
     # ---------------------------------------------------------------- embedding, convert
 

@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define DRIFT_ABI_VERSION 2
+#define DRIFT_ABI_VERSION 3
 
 /* Activation kinds: src/drift/runner/ops/Activation.scala:6-20. */
 enum {
@@ -245,6 +245,67 @@ int drift_qk_norm_rope_bf16(const uint16_t* q, const uint16_t* k, uint16_t* q_ou
                             int32_t heads, int32_t kv_heads, int32_t head_dim, float eps, float offset,
                             int32_t rotary, float theta, int32_t layout, int32_t sections, int32_t s0, int32_t s1,
                             int32_t s2, int32_t s3, void* stream);
+
+/* ---------------------------------------------------------------- attention inputs
+ * The paged KV cache (src/drift/runner/ops/KvCache.scala:5-22): keys F16
+ * (IEEE half bits in uint16_t) [cache_pages, page_size, kv_heads, head_dim],
+ * values F16 [cache_pages, kv_heads, head_dim, page_size] (transposed within
+ * a page); page_table (int32, table_pages entries) maps position / page_size
+ * to a page, position start + t holding token t. page_size must be a
+ * multiple of 16 (KvCache's rule) and table_pages * page_size >= start +
+ * tokens (ops/AttentionOps.scala:243-256). A page-table entry outside
+ * [0, cache_pages) writes nothing for its tokens and, when `bad_page`
+ * (device int32, nullable) is given, sets *bad_page = 1; the CPU reference
+ * fails on such an entry. F32 values are rounded to F16 to nearest even, as
+ * Float.floatToFloat16 does (F16 NaN payloads are the hardware's). */
+
+/* Keys and values [tokens, kv_heads, head_dim] into the cache at positions
+ * start .. start + tokens - 1. Replaces kernels/attention.hip:480-493
+ * cache_write (ops/HipAttention.scala cacheWrite; CPU
+ * ops/CpuAttention.scala:181-210). */
+int drift_cache_write_f32(const float* k, const float* v, uint16_t* keys, uint16_t* values,
+                          const int32_t* page_table, int32_t table_pages, int32_t cache_pages, int32_t tokens,
+                          int32_t kv_heads, int32_t head_dim, int32_t page_size, int32_t start, int32_t* bad_page,
+                          void* stream);
+int drift_cache_write_bf16(const uint16_t* k, const uint16_t* v, uint16_t* keys, uint16_t* values,
+                           const int32_t* page_table, int32_t table_pages, int32_t cache_pages, int32_t tokens,
+                           int32_t kv_heads, int32_t head_dim, int32_t page_size, int32_t start, int32_t* bad_page,
+                           void* stream);
+
+/* The halves of each row: x [rows, 2 d] into first and second [rows, d].
+ * Replaces kernels/linear_attention.hip:298-307 split_halves (CPU
+ * ops/CpuLayout.scala:137-143). */
+int drift_split_halves_f32(const float* x, float* first, float* second, int64_t rows, int32_t d, void* stream);
+int drift_split_halves_bf16(const uint16_t* x, uint16_t* first, uint16_t* second, int64_t rows, int32_t d,
+                            void* stream);
+
+/* A gated attention's inputs in one launch: each query head's row of
+ * query_and_gate [tokens, heads, 2 head_dim] is its query then its output
+ * gate (copied to gate [tokens, heads, head_dim]); the query is RMS-normed
+ * with q_norm (+ offset), as rmsNorm writes it in F32, and turned by the rope
+ * into queries [tokens, heads, head_dim]; each key head of k [tokens,
+ * kv_heads, head_dim] is normed with k_norm and turned, and written with its
+ * values v to the cache as cache_write does. With gate NULL, query_and_gate
+ * holds plain queries [tokens, heads, head_dim] (the dense decoders'
+ * norm + rope + cache write). Outputs may not alias inputs. Replaces
+ * kernels/attention.hip:495-536 attention_inputs (ops/HipAttention.scala:
+ * 144-215), the composition of ops/AttentionOps.scala:73-107 (splitHalves,
+ * rmsNorm, rmsNorm, rope, rope, cacheWrite). */
+int drift_attention_inputs_f32(const float* query_and_gate, const float* k, const float* v, const float* q_norm,
+                               const float* k_norm, float eps, float offset, const int32_t* positions,
+                               int32_t tokens, int32_t heads, int32_t kv_heads, int32_t head_dim, int32_t rotary,
+                               float theta, int32_t layout, int32_t sections, int32_t s0, int32_t s1, int32_t s2,
+                               int32_t s3, float* queries, float* gate, uint16_t* keys, uint16_t* values,
+                               const int32_t* page_table, int32_t table_pages, int32_t cache_pages, int32_t page_size,
+                               int32_t start, int32_t* bad_page, void* stream);
+int drift_attention_inputs_bf16(const uint16_t* query_and_gate, const uint16_t* k, const uint16_t* v,
+                                const float* q_norm, const float* k_norm, float eps, float offset,
+                                const int32_t* positions, int32_t tokens, int32_t heads, int32_t kv_heads,
+                                int32_t head_dim, int32_t rotary, float theta, int32_t layout, int32_t sections,
+                                int32_t s0, int32_t s1, int32_t s2, int32_t s3, uint16_t* queries, uint16_t* gate,
+                                uint16_t* keys, uint16_t* values, const int32_t* page_table, int32_t table_pages,
+                                int32_t cache_pages, int32_t page_size, int32_t start, int32_t* bad_page,
+                                void* stream);
 
 /* ---------------------------------------------------------------- embedding
  * Rows `ids` of a Q8_0 table ([vocab, cols], cols a multiple of 32: per 32

@@ -423,6 +423,72 @@ def embedding_q8_0_bf16(table, vocab, cols, ids):
     return to_bf16(embedding_q8_0(table, vocab, cols, ids))
 
 
+# ---------------------------------------------------------------- attention inputs
+
+def split_halves(x):
+    """CpuLayout.splitHalves (ops/CpuLayout.scala:137-143): rows [.., 2 d]
+    into their first and second halves."""
+    x = _c(x, np.float32)
+    d = x.shape[-1] // 2
+    return np.ascontiguousarray(x[..., :d]), np.ascontiguousarray(x[..., d:])
+
+
+def cache_place(page_table, page_size: int, position: int, kv_heads: int, dim: int, head: int, d: int):
+    """CpuAttention.cacheIndices (ops/CpuAttention.scala:163-179): the flat
+    indices of (position, head, d) in the keys and in the values."""
+    page = int(page_table[position // page_size])
+    offset = position % page_size
+    return (((page * page_size + offset) * kv_heads + head) * dim + d,
+            ((page * kv_heads + head) * dim + d) * page_size + offset)
+
+
+def cache_write(k, v, keys, values, page_table, page_size: int, start: int):
+    """CpuAttention.cacheWrite (ops/CpuAttention.scala:181-210): keys and
+    values [tokens, kv_heads, D] F32 into copies of the F16 cache (bits,
+    keys [pages, page_size, kv_heads, D], values [pages, kv_heads, D,
+    page_size]) at positions start .. start + tokens - 1; returns the copies.
+    Loops by element through cache_place, as the reference does."""
+    k, v = _c(k, np.float32), _c(v, np.float32)
+    tokens, kv_heads, dim = k.shape
+    keys, values = np.array(keys, np.uint16).reshape(-1), np.array(values, np.uint16).reshape(-1)
+    kf, vf = to_f16(k), to_f16(v)
+    for t in range(tokens):
+        for h in range(kv_heads):
+            for d in range(dim):
+                key_at, value_at = cache_place(page_table, page_size, start + t, kv_heads, dim, h, d)
+                keys[key_at] = kf[t, h, d]
+                values[value_at] = vf[t, h, d]
+    return keys, values
+
+
+def attention_inputs(query_and_gate, k, v, q_norm, k_norm, eps, offset, positions, theta, rotary, keys, values,
+                     page_table, page_size, start, layout=NEOX, sections=SINGLE, sizes=(), gated=True):
+    """The reference's attentionInputs composition (ops/AttentionOps.scala:
+    73-107): splitHalves of the gated query projection [t, heads, 2 D] (or,
+    with gated False, plain queries [t, heads, D]), rmsNorm of each query and
+    key head in place (F32 written), rope of both, cacheWrite of the rotated
+    keys with the values. Returns (rotated queries, gate or None, keys,
+    values), the cache as F16 bits."""
+    k = _c(k, np.float32)
+    if gated:
+        queries, gate = split_halves(query_and_gate)
+    else:
+        queries, gate = _c(query_and_gate, np.float32), None
+    rq, rk = qk_norm_rope(queries, k, q_norm, k_norm, positions, eps, offset, theta, rotary, layout, sections, sizes)
+    keys, values = cache_write(rk, v, keys, values, page_table, page_size, start)
+    return rq, gate, keys, values
+
+
+def attention_inputs_bf16(qg_bits, k_bits, v_bits, q_norm, k_norm, eps, offset, positions, theta, rotary, keys,
+                          values, page_table, page_size, start, layout=NEOX, sections=SINGLE, sizes=(), gated=True):
+    """The bf16 composition: inputs converted to F32, the F32 op, queries and
+    gate converted to BF16; the cache holds the F32 results rounded to F16."""
+    rq, gate, keys, values = attention_inputs(from_bf16(qg_bits), from_bf16(k_bits), from_bf16(v_bits), q_norm,
+                                              k_norm, eps, offset, positions, theta, rotary, keys, values,
+                                              page_table, page_size, start, layout, sections, sizes, gated)
+    return to_bf16(rq), None if gate is None else to_bf16(gate), keys, values
+
+
 # ---------------------------------------------------------------- inputs
 
 def java_gaussian(seed: int, count: int) -> np.ndarray:

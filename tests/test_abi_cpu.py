@@ -23,7 +23,7 @@ def test_header_and_library_agree(lib):
 
 
 def test_version_and_error_text(lib):
-    assert lib.drift_abi_version() == _lib.ABI_VERSION == 2
+    assert lib.drift_abi_version() == _lib.ABI_VERSION == 3
     assert lib.drift_error_string(0).decode().lower().startswith("no error")
     assert lib.drift_error_string(1)
 
@@ -106,3 +106,25 @@ def test_gated_residuals_refuse_bad_geometry(lib):
     assert "-3 rows" in refused(lib, "drift_row_gated_add_f32", p, p, p, -3, 8, NULL)
     assert "null operand" in refused(lib, "drift_row_gated_add_bf16", p, NULL, p, 3, 8, NULL)
     assert lib.drift_gated_add_f32(NULL, NULL, NULL, 0, 8, 1, NULL) == 0
+
+
+def test_attention_inputs_refuse_what_the_cache_checks_refuse(lib):
+    p = ctypes.c_void_p(16)
+    # cache_write(k, v, keys, values, table, table_pages, cache_pages, tokens, kv_heads, d, page_size, start, bad)
+    cw = lambda *g: (p, p, p, p, p, *g, NULL, NULL)
+    # KvCache: pages of a multiple of 16 tokens (ops/KvCache.scala:14-17)
+    assert "multiple of 16" in refused(lib, "drift_cache_write_f32", *cw(4, 4, 3, 2, 128, 10, 0))
+    # checkPageTable: the table covers start + tokens (ops/AttentionOps.scala:243-256)
+    assert "page table of 1 pages for 20 positions" in refused(lib, "drift_cache_write_bf16", *cw(1, 4, 6, 2, 128, 16, 14))
+    assert "start -1" in refused(lib, "drift_cache_write_f32", *cw(4, 4, 3, 2, 128, 16, -1))
+    assert lib.drift_cache_write_f32(NULL, NULL, NULL, NULL, NULL, 4, 4, 0, 2, 128, 16, 0, NULL, NULL) == 0
+    assert "rows of 2 x 0" in refused(lib, "drift_split_halves_f32", p, p, p, 4, 0, NULL)
+    assert lib.drift_split_halves_bf16(NULL, NULL, NULL, 0, 8, NULL) == 0
+    ai = lambda heads, kv, d, rotary, page_size, table_pages, start: (
+        p, p, p, p, p, 1e-6, 0.0, p, 3, heads, kv, d, rotary, 1e7, 0, 0, 0, 0, 0, 0, p, p, p, p, p, table_pages, 4,
+        page_size, start, NULL, NULL)
+    assert "rotary" in refused(lib, "drift_attention_inputs_f32", *ai(16, 2, 256, 257, 16, 4, 14))
+    assert "heads of 1024" in refused(lib, "drift_attention_inputs_bf16", *ai(16, 2, 1024, 64, 16, 4, 14))
+    assert "multiple of 16" in refused(lib, "drift_attention_inputs_f32", *ai(16, 2, 256, 64, 8, 4, 14))
+    assert "page table" in refused(lib, "drift_attention_inputs_f32", *ai(16, 2, 256, 64, 16, 1, 14))
+    assert "key heads" in refused(lib, "drift_attention_inputs_bf16", *ai(16, -2, 256, 64, 16, 4, 14))

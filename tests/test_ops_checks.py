@@ -106,3 +106,50 @@ def test_gated_residual_rules(hip):
     # a call that passes the rules stops at the device check
     with pytest.raises(ValueError, match="device memory"):
         hip.gatedAddChunk(f32(2, 4), f32(2, 4), f32(2, 24), 5)
+
+
+def f16(*shape):
+    return torch.zeros(shape, dtype=torch.float16)
+
+
+def i32(*shape):
+    return torch.zeros(shape, dtype=torch.int32)
+
+
+def test_the_cache_and_its_writes_are_checked(hip):
+    # ops/KvCache.scala:12-20: pages of a multiple of 16 tokens, F16
+    with pytest.raises(ValueError, match="pages of 10 tokens: not a multiple of 16"):
+        d.KvCache(f16(4, 10, 2, 8), f16(4, 2, 8, 10), 10)
+    with pytest.raises(ValueError, match="the cache is F16"):
+        d.KvCache(f32(4, 16, 2, 8), f16(4, 2, 8, 16), 16)
+    cache = d.KvCache(f16(4, 16, 2, 8), f16(4, 2, 8, 16), 16)
+    # ops/AttentionOps.scala:225-256
+    with pytest.raises(ValueError, match=r"cacheWrite: \[3, 3, 8\] into a cache of 2 heads of 8"):
+        hip.cacheWrite(f32(3, 3, 8), f32(3, 3, 8), cache, i32(4), 0)
+    with pytest.raises(ValueError, match="a page table of 1 pages for 19 positions"):
+        hip.cacheWrite(f32(3, 2, 8), f32(3, 2, 8), cache, i32(1), 16)
+    with pytest.raises(ValueError, match="a page table is I32"):
+        hip.cacheWrite(f32(3, 2, 8), f32(3, 2, 8), cache, f32(4), 0)
+    with pytest.raises(ValueError, match="equal shapes"):
+        hip.cacheWrite(f32(3, 2, 8), f32(2, 2, 8), cache, i32(4), 0)
+    with pytest.raises(ValueError, match="tensors live in device memory"):
+        hip.cacheWrite(f32(3, 2, 8), f32(3, 2, 8), cache, i32(4), 0)
+
+
+def test_split_halves_and_attention_inputs_are_checked(hip):
+    with pytest.raises(ValueError, match=r"splitHalves: \[2, 10\] into \[2, 4\]"):
+        hip.splitHalves(f32(2, 10), f32(2, 4), f32(2, 4))
+    cache = d.KvCache(f16(4, 16, 2, 8), f16(4, 2, 8, 16), 16)
+    norms = d.QueryKeyNorms(f32(8), f32(8), 1e-6, 0.0, d.Rope(1e4, 8))
+    t, heads = 3, 4
+    args = lambda qg, queries: (qg, f32(t, 2, 8), f32(t, 2, 8), norms, i32(t), cache, i32(4), 0, queries,
+                                f32(t, heads, 8), f32(t, 2, 8), f32(t, heads, 8))
+    with pytest.raises(ValueError, match="splitHalves"):
+        hip.attentionInputs(*args(f32(t, heads, 8), f32(t, heads, 8)))
+    with pytest.raises(ValueError, match="at most 512 fused"):
+        hip.attentionInputs(*args(f32(t, heads, 1024), f32(t, heads, 1024)))
+    with pytest.raises(ValueError, match="rope positions"):
+        hip.attentionInputs(f32(t, heads, 16), f32(t, 2, 8), f32(t, 2, 8), norms, i32(t + 1), cache, i32(4), 0,
+                            f32(t, heads, 8), f32(t, heads, 8), f32(t, 2, 8), f32(t, heads, 8))
+    with pytest.raises(ValueError, match="tensors live in device memory"):
+        hip.attentionInputs(*args(f32(t, heads, 16), f32(t, heads, 8)))
