@@ -4,7 +4,8 @@ A step is one pass of the path over its configurations, every kernel once:
   C2  decode bf16: RMSNorm [B, 4096] and SwiGLU [B, 14336], B = 1, 8, 64
       decode F32 with the int8 side output the products read: RMSNorm
       [B, 4096] and SwiGLU [B, 14336], B = 1, 64
-  C3  prefill bf16: per-head RMSNorm + NeoX RoPE, Q [4096, 32, 128], K [4096, 8, 128]
+  C3  prefill bf16: per-head RMSNorm + NeoX RoPE, Q [4096, 32, 128], K [4096, 8, 128]; and
+      the same with V [4096, 8, 128], keys and values written to a paged F16 KV cache
   C4  Q8_0 gather of 8192 ids from [151936, 4096] to bf16
   C5  Video DiT block bf16: AdaLN [65520, 3072], GELU-tanh in place, 3-D RoPE
       Q [65520, 24, 128] on the 21 x 30 x 52 grid; the gated residual with
@@ -202,6 +203,20 @@ def make_kernels(hip: d.HipOps):
                           lambda i, n=n: hip.queryKeyNormRope(qs[i % n], ks[i % n], norms, positions, rqs[i % n],
                                                               rks[i % n]), sets=n))
 
+    # The same prefill through the dense decoders' whole attention-input step:
+    # per-head norms, NeoX rope, and keys and values into the paged F16 cache
+    # (pages of 16 tokens, a shuffled page table)
+    vs = [randn_bf16((t, hk, dim), 450 + i) for i in range(n)]
+    pages = t // 16
+    caches = [d.KvCache.allocate(pages, 16, hk, dim, DEV) for _ in range(n)]
+    tables = [torch.randperm(pages, generator=gen(460 + i), device=DEV).to(torch.int32) for i in range(n)]
+    nbytes_ai = t * (2 * hq + 4 * hk) * dim * 2 + t * 4 + 2 * dim * 4 + pages * 4
+    kernels.append(Kernel("attention_inputs_bf16", "C3 with the KV-cache write: norms + NeoX RoPE of Q[4096,32,128] "
+                          "K[4096,8,128] bf16, K and V[4096,8,128] into a paged F16 cache", nbytes_ai, t,
+                          lambda i, n=n: hip.queryKeyNormRopeCache(qs[i % n], ks[i % n], vs[i % n], norms, positions,
+                                                                   caches[i % n], tables[i % n], 0, rqs[i % n]),
+                          sets=n))
+
     # C4: Q8_0 gather, 8192 ids from [151936, 4096] to bf16
     vocab, cols, count = 151936, 4096, 8192
     blocks = cols // 32
@@ -330,6 +345,15 @@ def cpu_baseline(kernels, budget_s: float):
         p = np.arange(units, dtype=np.int32)
         return lambda: o.qk_norm_rope_bf16(q, k, w128, w128, p, 1e-6, 0.0, 1e6, 128)
 
+    def attention_inputs(units):
+        q, k, v = bits((units, 32, 128)), bits((units, 8, 128)), bits((units, 8, 128))
+        p = np.arange(units, dtype=np.int32)
+        pages = -(-units // 16)
+        keys, values = np.zeros(pages * 16 * 8 * 128, np.uint16), np.zeros(pages * 8 * 128 * 16, np.uint16)
+        table = rng.permutation(pages).astype(np.int32)
+        return lambda: o.attention_inputs_bf16(q, k, v, w128, w128, 1e-6, 0.0, p, 1e6, 128, keys, values, table, 16,
+                                               0, gated=False)
+
     def gather(units):
         ids = rng.integers(0, 4096, units).astype(np.int32)
         return lambda: o.embedding_q8_0_bf16(table, 4096, 4096, ids)
@@ -379,13 +403,14 @@ def cpu_baseline(kernels, budget_s: float):
     for b in (1, 64):
         work[f"rms_norm_q8_f32_b{b}"] = (rms_q8, b, "rows")
         work[f"swiglu_q8_f32_b{b}"] = (swiglu_q8, b, "rows")
-    work.update({"qk_norm_rope_bf16": (qk, 4096, "tokens"), "embedding_q8_0_bf16": (gather, 8192, "ids"),
+    work.update({"qk_norm_rope_bf16": (qk, 4096, "tokens"), "attention_inputs_bf16": (attention_inputs, 4096, "tokens"),
+                 "embedding_q8_0_bf16": (gather, 8192, "ids"),
                  "adaln_bf16": (adaln, 65520, "rows"), "gelu_tanh_bf16": (gelu, 65520, "rows"),
                  "rope_3d_bf16": (rope3d, 65520, "tokens"), "gated_add_bf16": (gated_add, 65520, "rows"),
                  "modulate_chunks_bf16": (modulate_chunks, 65520, "rows"),
                  "gated_add_chunk_bf16": (gated_add_chunk, 65520, "rows"),
                  "row_gated_add_bf16": (row_gated_add, 65520 * 24, "head rows")})
-    # Each kernel gets 2/3 of budget_s / 11 seconds on one core: a sample of
+    # Each kernel gets 2/3 of budget_s / (kernels) seconds on one core: a sample of
     # up to the whole launch's units, run once untimed and then again until
     # that time is spent; the per-run time is what scales to the whole
     # launch. The all-cores leg gets the other third.

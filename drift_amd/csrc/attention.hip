@@ -43,6 +43,7 @@ struct Extras {
   const int32_t* page_table;
   int32_t pages, page_size, start;
   int32_t* bad_page;
+  int64_t tiles;  // value tiles the launch's extra blocks write (0: the token blocks write the values)
 };
 
 // Token t's place in the cache for key head kv: keys[key + d] and
@@ -170,6 +171,77 @@ __device__ __forceinline__ int qk_weight_slot(int d) {
   return d;
 }
 
+// Values into the cache by tiles: a tile is 16 consecutive positions of one
+// page (16 divides the page size) for one key head. The tile's values load
+// as chunks of N, go to LDS transposed ([value][position]) as F16, and leave
+// as 16-byte stores of 8 positions of one value: in the value layout
+// ([page][head][value][position]) a whole tile of a 16-token page is one
+// contiguous run. A position the tokens do not cover is left alone; a tile
+// of a page outside the cache writes nothing and sets *bad_page.
+constexpr int kQkMinThreads(int dim) { return dim < 64 ? 64 : (dim + 63) / 64 * 64; }
+
+// Key heads per value tile: as many as keep the staged tile within 4 KiB of
+// LDS (one head of 128; larger tiles measured slower, the kernel's LDS
+// holding fewer token blocks per CU).
+constexpr int kTileHeads(int dim) { return dim * 32 >= 4096 ? 1 : 4096 / (dim * 32); }
+
+template <typename T, int DIM, int H = kTileHeads(DIM)>
+__device__ __forceinline__ void cache_values_tile(const Extras<T>& e, int64_t tokens, int kv_heads, int64_t tile) {
+  constexpr int N = Chunk<T>::N;
+  constexpr int kTile = 16;
+  constexpr int kChunks = kTile * H * (DIM / N);
+  __shared__ __align__(16) uint16_t staged[H][DIM][kTile];
+  const int head_blocks = (kv_heads + H - 1) / H;
+  const int kv0 = (int)(tile % head_blocks) * H;
+  const int heads = min(H, kv_heads - kv0);
+  const int64_t first = (e.start / kTile + tile / head_blocks) * kTile;  // the tile's first position
+  const int64_t lo = max(first, (int64_t)e.start), hi = min(first + kTile, e.start + tokens);
+  // the values load first (their addresses do not need the page), positions
+  // the tokens do not cover and heads past the last clamped to ones they do
+  // (a launch's blocks have at least max(64, DIM) threads)
+  constexpr int kPerThread = (kChunks + kQkMinThreads(DIM) - 1) / kQkMinThreads(DIM);
+  typename Chunk<T>::Raw raw[kPerThread];
+#pragma unroll
+  for (int r = 0; r < kPerThread; ++r) {
+    const int c = (int)threadIdx.x + r * (int)blockDim.x;
+    if (c < kChunks) {
+      const int i = c / (H * (DIM / N)), hh = min(c / (DIM / N) % H, heads - 1), d = (c % (DIM / N)) * N;
+      const int64_t position = min(max(first + i, lo), hi - 1);
+      raw[r] = Chunk<T>::load_raw(e.v + ((position - e.start) * kv_heads + kv0 + hh) * DIM + d);
+    }
+  }
+  const int64_t page = e.page_table[first / e.page_size];
+#pragma unroll
+  for (int r = 0; r < kPerThread; ++r) {
+    const int c = (int)threadIdx.x + r * (int)blockDim.x;
+    if (c >= kChunks) break;
+    const int i = c / (H * (DIM / N)), hh = c / (DIM / N) % H, d = (c % (DIM / N)) * N;
+    float v[N];
+    Chunk<T>::unpack(raw[r], v);
+#pragma unroll
+    for (int j = 0; j < N; ++j) staged[hh][d + j][i] = (uint16_t)f16_bits(v[j]);
+  }
+  __syncthreads();
+  if (page < 0 || page >= e.pages) {
+    if (e.bad_page && threadIdx.x == 0) *e.bad_page = 1;
+    return;
+  }
+  // rows (head, value) of the tile: kv0's row 0, then on, page_size apart
+  uint16_t* row0 = e.values + (page * kv_heads + kv0) * (int64_t)DIM * e.page_size + first % e.page_size;
+  if (lo == first && hi == first + kTile) {
+    for (int c = threadIdx.x; c < heads * DIM * 2; c += blockDim.x) {
+      const int row = c / 2, i = (c % 2) * 8;
+      const uint4 w = *reinterpret_cast<const uint4*>(&staged[row / DIM][row % DIM][i]);
+      *reinterpret_cast<uint4*>(row0 + (int64_t)row * e.page_size + i) = w;
+    }
+  } else {
+    for (int c = threadIdx.x; c < heads * DIM * kTile; c += blockDim.x) {
+      const int row = c / kTile, i = c % kTile;
+      if (first + i >= lo && first + i < hi) row0[(int64_t)row * e.page_size + i] = staged[row / DIM][row % DIM][i];
+    }
+  }
+}
+
 constexpr int kQkMaxWaves = 16;
 
 template <typename T, int G, bool NEOX, bool EXTRAS>
@@ -186,6 +258,13 @@ __global__ void __launch_bounds__(kQkMaxWaves * 64) qk_norm_rope_token(const T* 
   const RopeArgs& p = a.rope;
   constexpr int dim = 2 * N * G, half = N * G;
   const int64_t t = blockIdx.x;
+  if constexpr (EXTRAS) {
+    // with the cache, blocks past the tokens' write the values by tiles
+    if (t >= p.tokens) {
+      cache_values_tile<T, dim>(e, p.tokens, a.kv_heads, t - p.tokens);
+      return;
+    }
+  }
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int waves = blockDim.x >> 6;
   const int rows = a.q_heads + a.kv_heads;
@@ -209,19 +288,14 @@ __global__ void __launch_bounds__(kQkMaxWaves * 64) qk_norm_rope_token(const T* 
   const T* xh = input_at(min(h, rows - 1));
   Raw r0 = Chunk<T>::load_raw(xh + d0);
   Raw r1 = Chunk<T>::load_raw(xh + d1);
-  // the gate half of a query head's row; the values of a key head's (rows
-  // past the last of their kind are clamped to it)
-  Raw g0, g1, u0, u1;
+  // the gate half of a query head's row (rows past the last query head are
+  // clamped to it)
+  Raw g0, g1;
   auto load_extras = [&](int hh) {
     if (e.gate && a.q_heads > 0) {
       const T* gh = q + (t * a.q_heads + min(hh, a.q_heads - 1)) * a.q_stride + dim;
       g0 = Chunk<T>::load_raw(gh + d0);
       g1 = Chunk<T>::load_raw(gh + d1);
-    }
-    if (e.keys && a.kv_heads > 0) {
-      const T* vh = e.v + (t * a.kv_heads + min(max(hh - a.q_heads, 0), a.kv_heads - 1)) * dim;
-      u0 = Chunk<T>::load_raw(vh + d0);
-      u1 = Chunk<T>::load_raw(vh + d1);
     }
   };
   if constexpr (EXTRAS) load_extras(h);
@@ -288,14 +362,6 @@ __global__ void __launch_bounds__(kQkMaxWaves * 64) qk_norm_rope_token(const T* 
         if (!query && e.keys && cache_place(e, t, a.kv_heads, dim, h - a.q_heads, key, value)) {
           store_f16<N>(e.keys + key + d0, v0);
           store_f16<N>(e.keys + key + d1, v1);
-          float w0[N], w1[N];
-          Chunk<T>::unpack(u0, w0);
-          Chunk<T>::unpack(u1, w1);
-#pragma unroll
-          for (int i = 0; i < N; ++i) {
-            e.values[value + (int64_t)(d0 + i) * e.page_size] = (uint16_t)f16_bits(w0[i]);
-            e.values[value + (int64_t)(d1 + i) * e.page_size] = (uint16_t)f16_bits(w1[i]);
-          }
         }
       }
     }
@@ -404,16 +470,23 @@ int qk_launch(const char* entry, const T* q, const T* k, T* q_out, T* k_out, con
   // a wave per 64 / G heads, and a thread per weight of a head
   const int waves = (int)std::min<int64_t>(
       kQkMaxWaves, std::max<int64_t>(ceil_div(a.q_heads + a.kv_heads, heads_per_wave), ceil_div(dim, kWave)));
-  const dim3 grid(p.tokens), block(64 * waves);
+  // with the cache, blocks past the tokens write the values by tiles of 16
+  // positions and one key head
+  Extras<T> ex = e;
+  const int tile_heads = kTileHeads(dim);
+  ex.tiles = EXTRAS && e.keys ? ((int64_t)(e.start + p.tokens - 1) / 16 - e.start / 16 + 1) *
+                                    ((a.kv_heads + tile_heads - 1) / tile_heads)
+                              : 0;
+  const dim3 grid((unsigned)(p.tokens + ex.tiles)), block(64 * waves);
   switch (lanes_per_head) {
 #define DRIFT_QK_CASE(G)                                                                                             \
   case G:                                                                                                            \
     if (p.layout == DRIFT_ROPE_NEOX)                                                                                 \
       hipLaunchKernelGGL((qk_norm_rope_token<T, G, true, EXTRAS>), grid, block, 0, st, q, k, q_out, k_out, q_weight, \
-                         k_weight, positions, a, e);                                                                 \
+                         k_weight, positions, a, ex);                                                                 \
     else                                                                                                             \
       hipLaunchKernelGGL((qk_norm_rope_token<T, G, false, EXTRAS>), grid, block, 0, st, q, k, q_out, k_out,          \
-                         q_weight, k_weight, positions, a, e);                                                       \
+                         q_weight, k_weight, positions, a, ex);                                                       \
     break;
     DRIFT_QK_CASE(1)
     DRIFT_QK_CASE(2)
@@ -484,10 +557,10 @@ int attention_inputs(const char* entry, const T* query_and_gate, const T* k, con
   a.eps = eps;
   a.offset = offset;
   a.q_stride = gate ? 2 * (int64_t)dim : dim;
-  const Extras<T> e{gate, v, keys, values, page_table, cache_pages, page_size, start, bad_page};
+  const Extras<T> e{gate, v, keys, values, page_table, cache_pages, page_size, start, bad_page, 0};
   const bool aligned = (!query_and_gate || (aligned16(query_and_gate) && aligned16(queries))) &&
                        (!gate || aligned16(gate)) && (!k || (aligned16(k) && aligned16(v))) &&
-                       (!keys || aligned16(keys));
+                       (!keys || (aligned16(keys) && aligned16(values)));
   return qk_launch<T, true>(entry, query_and_gate, k, queries, nullptr, q_norm, k_norm, positions, a, e, aligned,
                             (hipStream_t)stream);
 }
@@ -507,7 +580,7 @@ int cache_write(const char* entry, const T* k, const T* v, uint16_t* keys, uint1
                   (long long)start + tokens);
   if ((int64_t)tokens * kv_heads == 0) return 0;
   if (!k || !v || !keys || !values || !page_table) return refuse("%s: null tensor", entry);
-  const Extras<T> e{nullptr, v, keys, values, page_table, cache_pages, page_size, start, bad_page};
+  const Extras<T> e{nullptr, v, keys, values, page_table, cache_pages, page_size, start, bad_page, 0};
   constexpr int N = Chunk<T>::N;
   const hipStream_t st = (hipStream_t)stream;
   const int64_t values_count = (int64_t)tokens * kv_heads * dim;

@@ -447,17 +447,18 @@ def cache_write(k, v, keys, values, page_table, page_size: int, start: int):
     values [tokens, kv_heads, D] F32 into copies of the F16 cache (bits,
     keys [pages, page_size, kv_heads, D], values [pages, kv_heads, D,
     page_size]) at positions start .. start + tokens - 1; returns the copies.
-    Loops by element through cache_place, as the reference does."""
+    Every element's indices are cache_place's formula, taken over all
+    (t, head, d) at once."""
     k, v = _c(k, np.float32), _c(v, np.float32)
     tokens, kv_heads, dim = k.shape
     keys, values = np.array(keys, np.uint16).reshape(-1), np.array(values, np.uint16).reshape(-1)
-    kf, vf = to_f16(k), to_f16(v)
-    for t in range(tokens):
-        for h in range(kv_heads):
-            for d in range(dim):
-                key_at, value_at = cache_place(page_table, page_size, start + t, kv_heads, dim, h, d)
-                keys[key_at] = kf[t, h, d]
-                values[value_at] = vf[t, h, d]
+    position = start + np.arange(tokens, dtype=np.int64)[:, None, None]
+    page = np.asarray(page_table, np.int64)[position // page_size]
+    offset = position % page_size
+    head = np.arange(kv_heads, dtype=np.int64)[None, :, None]
+    d = np.arange(dim, dtype=np.int64)[None, None, :]
+    keys[((page * page_size + offset) * kv_heads + head) * dim + d] = to_f16(k)
+    values[((page * kv_heads + head) * dim + d) * page_size + offset] = to_f16(v)
     return keys, values
 
 
