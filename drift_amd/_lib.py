@@ -68,10 +68,14 @@ SIGNATURES = {
                                            _I32, _P, _P]),
     "drift_embedding_q8_0_f32": (_I32, [_P, _P, _P, _I64, _I64, _I32, _P, _P]),
     "drift_embedding_q8_0_bf16": (_I32, [_P, _P, _P, _I64, _I64, _I32, _P, _P]),
+    "drift_embedding_f32": (_I32, [_P, _I32, _P, _P, _I64, _I64, _I32, _P, _P]),
+    "drift_embedding_bf16": (_I32, [_P, _I32, _P, _P, _I64, _I64, _I32, _P, _P]),
+    "drift_dequantize_bf16": (_I32, [_P, _I32, _P, _I64, _I32, _P]),
+    "drift_dequantize_f16": (_I32, [_P, _I32, _P, _I64, _I32, _P]),
     "drift_convert": (_I32, [_P, _P, _I64, _I32, _P]),
 }
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 
 class NotBuilt(RuntimeError):

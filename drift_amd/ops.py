@@ -129,17 +129,52 @@ class KvCache:
                        torch.empty((pages, kvHeads, headDimension, pageSize), dtype=F16, device=device), pageSize)
 
 
+@dataclass(frozen=True)
+class StorageType:
+    """A table's storage type (tensor/DType.scala:14-66): `values` per block
+    of `bytes`, its GGUF type id (the kernels' `format`), and the alignment
+    its blocks' fields need."""
+    name: str
+    ggmlId: int
+    values: int
+    bytes: int
+    align: int
+
+    def rowBytes(self, cols: int) -> int:
+        _require(cols % self.values == 0, f"{cols} elements are not whole {self.name} blocks of {self.values}")
+        return cols // self.values * self.bytes
+
+
+# tensor/DType.scala, GgmlQuants.scala:12-118, KQuants.scala:100-134,
+# IQuants.scala:40-80, RocmFp4.scala:75-84: the types with gather kernels
+# (kernels/matvec.hip:942-954), and F32, F16, BF16.
+STORAGE_TYPES = {t.name: t for t in (
+    StorageType("F32", 0, 1, 4, 16), StorageType("F16", 1, 1, 2, 16), StorageType("BF16", 30, 1, 2, 16),
+    StorageType("Q4_0", 2, 32, 18, 2), StorageType("Q4_1", 3, 32, 20, 4), StorageType("Q5_0", 6, 32, 22, 2),
+    StorageType("Q5_1", 7, 32, 24, 4), StorageType("Q8_0", 8, 32, 34, 2), StorageType("Q4_K", 12, 256, 144, 8),
+    StorageType("Q5_K", 13, 256, 176, 8), StorageType("Q6_K", 14, 256, 210, 2),
+    StorageType("IQ4_NL", 20, 32, 18, 2), StorageType("IQ4_XS", 23, 256, 136, 8),
+    StorageType("Q4_0_ROCMFP4", 100, 32, 18, 2), StorageType("Q4_0_ROCMFP4_FAST", 101, 32, 17, 1))}
+
+
 @dataclass
-class Q8_0Table:
-    """A Q8_0 table ([vocabulary, cols] values) as its bytes: a uint8 tensor
-    [vocabulary, cols / 32 * 34], per 32 values an fp16 scale then 32 int8
-    codes (tensor/GgmlQuants.scala:104-118)."""
+class StoredTable:
+    """A table ([vocabulary, cols] values) as its stored bytes: a uint8
+    tensor [vocabulary, row bytes] in storage type `dtype` (a GGUF tensor's
+    data as it lies in the file)."""
     data: torch.Tensor
+    dtype: StorageType
     cols: int
 
     @property
     def shape(self) -> tuple:
         return (self.data.shape[0], self.cols)
+
+
+def Q8_0Table(data: torch.Tensor, cols: int) -> StoredTable:
+    """A Q8_0 table: per 32 values an fp16 scale then 32 int8 codes
+    (tensor/GgmlQuants.scala:104-118), [vocabulary, cols / 32 * 34] bytes."""
+    return StoredTable(data, STORAGE_TYPES["Q8_0"], cols)
 
 
 @dataclass(frozen=True)
@@ -700,20 +735,43 @@ class HipOps:
 
     # ---------------------------------------------------------------- embedding, convert
 
-    def embedding(self, table: Q8_0Table, ids, out, badId: Optional[torch.Tensor] = None) -> None:
-        """Rows `ids` of a Q8_0 table, decoded (ops/LinearOps.scala:16). An id
-        outside the table (which the reference refuses) gets a zero row and
-        sets `badId` (int32 [1], device) to 1 when given."""
+    def embedding(self, table: StoredTable, ids, out, badId: Optional[torch.Tensor] = None) -> None:
+        """Rows `ids` of a table, decoded (ops/LinearOps.scala:16), into out
+        F32 or BF16. An id outside the table (which the reference refuses)
+        gets a zero row and sets `badId` (int32 [1], device) to 1 when given."""
         checkEmbedding(table, ids, out)
-        _require(isinstance(table, Q8_0Table), "embedding: only Q8_0 tables have kernels here")
-        vocab, cols = table.shape
-        _require(cols % 32 == 0, f"{cols} elements are not whole Q8_0 blocks of 32")
-        _require(tuple(table.data.shape) == (vocab, cols // 32 * 34) and table.data.dtype == torch.uint8,
-                 f"embedding: Q8_0 bytes {_shape(table.data)} for rows of {cols}")
-        _require(table.data.is_contiguous(), "embedding: Q8_0 bytes must be contiguous rows")
+        t = self._checkStored("embedding", table)
+        _require(table.cols % 8 == 0, f"embedding: rows of {table.cols} values (kernels take multiples of 8)")
         _on_device("embedding", table.data, ids, out)
-        self._launch(f"drift_embedding_q8_0_{_suffix(out.dtype)}", _ptr(table.data), _ptr(ids), _ptr(out),
-                     ids.shape[0], vocab, cols, _ptr(badId))
+        vocab, cols = table.shape
+        if t.name == "Q8_0":
+            self._launch(f"drift_embedding_q8_0_{_suffix(out.dtype)}", _ptr(table.data), _ptr(ids), _ptr(out),
+                         ids.shape[0], vocab, cols, _ptr(badId))
+        else:
+            self._launch(f"drift_embedding_{_suffix(out.dtype)}", _ptr(table.data), t.ggmlId, _ptr(ids), _ptr(out),
+                         ids.shape[0], vocab, cols, _ptr(badId))
+
+    def dequantize(self, table: StoredTable, out) -> None:
+        """The whole table decoded into out [rows, cols], BF16 or F16, for
+        the GEMM path (kernels/matvec.hip:801-827 dequantize, dequantize_bf16)."""
+        t = self._checkStored("dequantize", table)
+        _require(out.dtype in (BF16, F16), f"dequantize writes BF16 or F16, not {_name(out.dtype)}")
+        _require(tuple(out.shape) == table.shape, f"dequantize: out {_shape(out)} for a table {list(table.shape)}")
+        _require(table.cols % 8 == 0, f"dequantize: rows of {table.cols} values (kernels take multiples of 8)")
+        _on_device("dequantize", table.data, out)
+        entry = "drift_dequantize_bf16" if out.dtype == BF16 else "drift_dequantize_f16"
+        self._launch(entry, _ptr(table.data), t.ggmlId, _ptr(out), table.shape[0], table.cols)
+
+    @staticmethod
+    def _checkStored(operation: str, table: StoredTable) -> StorageType:
+        _require(isinstance(table, StoredTable), f"{operation}: a table of stored bytes")
+        t = table.dtype
+        vocab, cols = table.shape
+        _require(cols % t.values == 0, f"{cols} elements are not whole {t.name} blocks of {t.values}")
+        _require(table.data.dtype == torch.uint8 and tuple(table.data.shape) == (vocab, t.rowBytes(cols)),
+                 f"{operation}: {t.name} bytes {_shape(table.data)} for rows of {cols}")
+        _require(table.data.is_contiguous(), f"{operation}: {t.name} bytes must be contiguous rows")
+        return t
 
     def convert(self, x, out) -> None:
         """ops/MemoryOps.scala:46."""

@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define DRIFT_ABI_VERSION 3
+#define DRIFT_ABI_VERSION 4
 
 /* Activation kinds: src/drift/runner/ops/Activation.scala:6-20. */
 enum {
@@ -55,6 +55,27 @@ enum {
   DRIFT_SECTIONS_CONTIGUOUS = 1,
   DRIFT_SECTIONS_INTERLEAVED = 2,
   DRIFT_SECTIONS_AXES = 3
+};
+
+/* Storage types of tables, by their GGUF type ids (the ggmlId of
+ * src/drift/runner/tensor/DType.scala, GgmlQuants.scala, KQuants.scala,
+ * IQuants.scala, RocmFp4.scala). */
+enum {
+  DRIFT_F32 = 0,
+  DRIFT_F16 = 1,
+  DRIFT_Q4_0 = 2,
+  DRIFT_Q4_1 = 3,
+  DRIFT_Q5_0 = 6,
+  DRIFT_Q5_1 = 7,
+  DRIFT_Q8_0 = 8,
+  DRIFT_Q4_K = 12,
+  DRIFT_Q5_K = 13,
+  DRIFT_Q6_K = 14,
+  DRIFT_IQ4_NL = 20,
+  DRIFT_IQ4_XS = 23,
+  DRIFT_BF16 = 30,
+  DRIFT_Q4_0_ROCMFP4 = 100,
+  DRIFT_Q4_0_ROCMFP4_FAST = 101
 };
 
 /* Conversions: src/drift/runner/ops/HipBase.scala:268-274 (codes of
@@ -322,6 +343,32 @@ int drift_embedding_q8_0_f32(const uint8_t* table, const int32_t* ids, float* ou
                              int32_t cols, int32_t* bad_id, void* stream);
 int drift_embedding_q8_0_bf16(const uint8_t* table, const int32_t* ids, uint16_t* out, int64_t count,
                               int64_t vocab, int32_t cols, int32_t* bad_id, void* stream);
+
+/* Rows `ids` of a table of storage type `format` ([vocab, cols] values, each
+ * row whole blocks: 32 values for the 32-value quants, 256 for the K-quants
+ * and IQ4_XS, cols a multiple of 8), decoded as the type's decoder in the
+ * reference does (bit-exact, BF16 the F32 value rounded to nearest even),
+ * into out [count, cols]. The table must be aligned to its blocks' fields
+ * (2 bytes for Q4_0, Q5_0, Q8_0, Q6_K, IQ4_NL, ROCmFP4; 4 for Q4_1, Q5_1; 8
+ * for Q4_K, Q5_K, IQ4_XS; 1 for ROCmFP4 fast; 16 for F32, F16, BF16) and out
+ * 16-byte aligned. Ids outside [0, vocab) as drift_embedding_q8_0 (which Q8_0
+ * tables take). Replaces kernels/matvec.hip:830-839 gather<T> and its
+ * gather_<q> instances (:891-897, :942-954) and elementwise.hip:89-93
+ * gather_rows_f32 (ops/HipLinear.scala:21-52; CPU ops/CpuLinear.scala:12-41). */
+int drift_embedding_f32(const void* table, int32_t format, const int32_t* ids, float* out, int64_t count,
+                        int64_t vocab, int32_t cols, int32_t* bad_id, void* stream);
+int drift_embedding_bf16(const void* table, int32_t format, const int32_t* ids, uint16_t* out, int64_t count,
+                         int64_t vocab, int32_t cols, int32_t* bad_id, void* stream);
+
+/* A whole table of storage type `format` ([rows, cols]) decoded into out
+ * [rows, cols] as BF16 (nearest even) or F16 (IEEE half bits, nearest even),
+ * for the GEMM path. Same layout rules as drift_embedding_f32. Replaces
+ * kernels/matvec.hip:814-827 dequantize_bf16<T> and :801-812 dequantize<T>
+ * (their dequantize_bf16_<q> and dequantize_<q> instances, :891-893). */
+int drift_dequantize_bf16(const void* table, int32_t format, uint16_t* out, int64_t rows, int32_t cols,
+                          void* stream);
+int drift_dequantize_f16(const void* table, int32_t format, uint16_t* out, int64_t rows, int32_t cols,
+                         void* stream);
 
 /* ---------------------------------------------------------------- convert
  * Elementwise type conversion of n values (kinds above). Replaces

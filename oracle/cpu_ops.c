@@ -381,6 +381,211 @@ int64_t oracle_embedding_f32(const float* table, int64_t vocab, int64_t cols, co
   return -1;
 }
 
+/* ---- storage types: tensor/GgmlQuants.scala, tensor/KQuants.scala,
+ * tensor/IQuants.scala, tensor/RocmFp4.scala, tensor/DType.scala. Each
+ * decoder restates the Scala's decodeBlock (or its per-element formula),
+ * operation by operation in float, as the JVM evaluates it (no contraction:
+ * the Makefile's -ffp-contract=off). ---- */
+
+static uint32_t u8_at(const uint8_t* p, int64_t at) { return p[at]; }
+static int32_t i8_at(const uint8_t* p, int64_t at) { return (int8_t)p[at]; }
+static uint32_t u16_at(const uint8_t* p, int64_t at) { return (uint32_t)p[at] | ((uint32_t)p[at + 1] << 8); }
+static uint32_t u32_at(const uint8_t* p, int64_t at) { return u16_at(p, at) | (u16_at(p, at + 2) << 16); }
+static float f16_at(const uint8_t* p, int64_t at) { return oracle_f16_to_f32((uint16_t)u16_at(p, at)); }
+
+/* GgmlQuants.fiveBit (GgmlQuants.scala:53-64) */
+static int five_bit(const uint8_t* b, int64_t qh_at, int64_t qs_at, int j) {
+  const uint32_t qh = u32_at(b, qh_at);
+  const uint32_t nibbles = u8_at(b, qs_at + (j % 16));
+  const uint32_t low = j < 16 ? (nibbles & 0xf) : (nibbles >> 4);
+  return (int)(low | (((qh >> j) & 1u) << 4));
+}
+
+/* KQuants.twoBits, nibble, scaleAndMin (KQuants.scala:38-70) */
+static int two_bits(const uint8_t* b, int64_t at, int e) {
+  const int half = e / 128, plane = (e % 128) / 32;
+  return (int)((u8_at(b, at + half * 32 + e % 32) >> (2 * plane)) & 3u);
+}
+
+static int nibble_k(const uint8_t* b, int64_t at, int e) {
+  const int chunk = e / 32;
+  return (int)((u8_at(b, at + (chunk / 2) * 32 + e % 32) >> (4 * (chunk % 2))) & 0xfu);
+}
+
+static void scale_and_min(const uint8_t* b, int64_t at, int j, int* scale, int* min) {
+#define BYTE(i) ((int)u8_at(b, at + (i)))
+  if (j < 4) {
+    *scale = BYTE(j) & 63;
+    *min = BYTE(j + 4) & 63;
+  } else {
+    *scale = (BYTE(j + 4) & 0xf) | ((BYTE(j - 4) >> 2) & 0x30);
+    *min = (BYTE(j + 4) >> 4) | ((BYTE(j) >> 2) & 0x30);
+  }
+#undef BYTE
+}
+
+/* IQuants.Values (IQuants.scala:14-16) */
+static const float kIq4Values[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+
+/* RocmFp4.Codebook and halfScale (RocmFp4.scala:21-39) */
+static const float kRocmCodebook[16] = {0, 1, 2, 3, 4, 6, 8, 10, 0, -1, -2, -3, -4, -6, -8, -10};
+
+float oracle_rocmfp4_half_scale(int byte) {
+  if (byte > 0x7e) return 0.0f;
+  const int exponent = byte >> 3, mantissa = byte & 7;
+  if (exponent == 0) return ldexpf((float)mantissa, -10);
+  return (float)(8 + mantissa) * ldexpf(1.0f, exponent - 11);
+}
+
+int oracle_format_block(int format, int* block_values, int* block_bytes) {
+  int v = 32, n;
+  switch (format) {
+    case ORACLE_F32: v = 1; n = 4; break;
+    case ORACLE_F16: case ORACLE_BF16: v = 1; n = 2; break;
+    case ORACLE_Q4_0: n = 18; break;
+    case ORACLE_Q4_1: n = 20; break;
+    case ORACLE_Q5_0: n = 22; break;
+    case ORACLE_Q5_1: n = 24; break;
+    case ORACLE_Q8_0: n = 34; break;
+    case ORACLE_Q4_K: v = 256; n = 144; break;
+    case ORACLE_Q5_K: v = 256; n = 176; break;
+    case ORACLE_Q6_K: v = 256; n = 210; break;
+    case ORACLE_IQ4_NL: n = 18; break;
+    case ORACLE_IQ4_XS: v = 256; n = 136; break;
+    case ORACLE_ROCMFP4: n = 18; break;
+    case ORACLE_ROCMFP4_FAST: n = 17; break;
+    default: return -1;
+  }
+  *block_values = v;
+  *block_bytes = n;
+  return 0;
+}
+
+/* One block of `format` at b into out (block_values values). */
+static void decode_block(int format, const uint8_t* b, float* out) {
+  switch (format) {
+    case ORACLE_F32: { uint32_t w = u32_at(b, 0); memcpy(out, &w, 4); return; }
+    case ORACLE_F16: out[0] = f16_at(b, 0); return;
+    case ORACLE_BF16: out[0] = oracle_from_bf16((uint16_t)u16_at(b, 0)); return;
+    case ORACLE_Q4_0: { /* GgmlQuants.scala:13-29: d * (q - 8) */
+      const float d = f16_at(b, 0);
+      for (int j = 0; j < 16; ++j) {
+        const uint32_t byte = u8_at(b, 2 + j);
+        out[j] = d * (float)((int)(byte & 0xf) - 8);
+        out[j + 16] = d * (float)((int)(byte >> 4) - 8);
+      }
+      return;
+    }
+    case ORACLE_Q4_1: { /* :31-49: d * q + m */
+      const float d = f16_at(b, 0), m = f16_at(b, 2);
+      for (int j = 0; j < 16; ++j) {
+        const uint32_t byte = u8_at(b, 4 + j);
+        out[j] = d * (float)(byte & 0xf) + m;
+        out[j + 16] = d * (float)(byte >> 4) + m;
+      }
+      return;
+    }
+    case ORACLE_Q5_0: { /* :66-81: d * (q - 16) */
+      const float d = f16_at(b, 0);
+      for (int j = 0; j < 32; ++j) out[j] = d * (float)(five_bit(b, 2, 6, j) - 16);
+      return;
+    }
+    case ORACLE_Q5_1: { /* :83-99: d * q + m */
+      const float d = f16_at(b, 0), m = f16_at(b, 2);
+      for (int j = 0; j < 32; ++j) out[j] = d * (float)five_bit(b, 4, 8, j) + m;
+      return;
+    }
+    case ORACLE_Q8_0: { /* :101-117: q * d */
+      const float d = f16_at(b, 0);
+      for (int j = 0; j < 32; ++j) out[j] = (float)i8_at(b, 2 + j) * d;
+      return;
+    }
+    case ORACLE_Q4_K: /* KQuants.scala:102-110: d * sc * q - dmin * m, per 32 */
+      for (int e = 0; e < 256; ++e) {
+        int scale, min;
+        scale_and_min(b, 4, e / 32, &scale, &min);
+        const float d = f16_at(b, 0) * (float)scale;
+        const float m = f16_at(b, 2) * (float)min;
+        out[e] = d * (float)nibble_k(b, 16, e) - m;
+      }
+      return;
+    case ORACLE_Q5_K: /* :112-121 */
+      for (int e = 0; e < 256; ++e) {
+        int scale, min;
+        scale_and_min(b, 4, e / 32, &scale, &min);
+        const float d = f16_at(b, 0) * (float)scale;
+        const float m = f16_at(b, 2) * (float)min;
+        const int high = (int)((u8_at(b, 16 + e % 32) >> (e / 32)) & 1u);
+        out[e] = d * (float)(nibble_k(b, 48, e) | (high << 4)) - m;
+      }
+      return;
+    case ORACLE_Q6_K: /* :123-134: d * sc * (q - 32) */
+      for (int e = 0; e < 256; ++e) {
+        const int half = e / 128, r = e % 128;
+        const int low = (int)((u8_at(b, half * 64 + r % 64) >> (4 * (r / 64))) & 0xfu);
+        const int q = (low | (two_bits(b, 128, e) << 4)) - 32;
+        const float d = f16_at(b, 208) * (float)i8_at(b, 192 + e / 16);
+        out[e] = d * (float)q;
+      }
+      return;
+    case ORACLE_IQ4_NL: { /* IQuants.scala:18-47 */
+      const float d = f16_at(b, 0);
+      for (int j = 0; j < 16; ++j) {
+        const uint32_t byte = u8_at(b, 2 + j);
+        out[j] = d * kIq4Values[byte & 0xf];
+        out[j + 16] = d * kIq4Values[byte >> 4];
+      }
+      return;
+    }
+    case ORACLE_IQ4_XS: { /* :49-80 */
+      const float d = f16_at(b, 0);
+      const uint32_t high = u16_at(b, 2);
+      for (int i = 0; i < 8; ++i) {
+        const uint32_t low = (u8_at(b, 4 + i / 2) >> (4 * (i % 2))) & 0xf;
+        const int ls = (int)(low | (((high >> (2 * i)) & 3u) << 4));
+        const float scale = d * (float)(ls - 32);
+        for (int j = 0; j < 16; ++j) {
+          const uint32_t byte = u8_at(b, 8 + 16 * i + j);
+          out[32 * i + j] = scale * kIq4Values[byte & 0xf];
+          out[32 * i + j + 16] = scale * kIq4Values[byte >> 4];
+        }
+      }
+      return;
+    }
+    default: { /* ROCmFP4, RocmFp4.scala:45-62: scales at 16 and 17 (dual) or 16 (fast) */
+      const float low = oracle_rocmfp4_half_scale((int)u8_at(b, 16));
+      const float high = oracle_rocmfp4_half_scale((int)u8_at(b, format == ORACLE_ROCMFP4 ? 17 : 16));
+      for (int j = 0; j < 16; ++j) {
+        const uint32_t byte = u8_at(b, j);
+        out[j] = kRocmCodebook[byte & 0xf] * low;
+        out[j + 16] = kRocmCodebook[byte >> 4] * high;
+      }
+      return;
+    }
+  }
+}
+
+int oracle_decode_row(int format, const uint8_t* row, int64_t cols, float* out) {
+  int values, bytes;
+  if (oracle_format_block(format, &values, &bytes) != 0 || cols % values != 0) return -1;
+  for (int64_t b = 0; b < cols / values; ++b) decode_block(format, row + b * bytes, out + b * values);
+  return 0;
+}
+
+/* ops/CpuLinear.scala:12-41 with any storage type: decoded rows as F32. */
+int64_t oracle_embedding(int format, const uint8_t* table, int64_t vocab, int64_t cols, const int32_t* ids,
+                         int64_t count, float* out) {
+  int values, bytes;
+  if (oracle_format_block(format, &values, &bytes) != 0 || cols % values != 0) return -2;
+  const int64_t row_bytes = cols / values * bytes;
+  for (int64_t t = 0; t < count; ++t) {
+    const int64_t row = ids[t];
+    if (row < 0 || row >= vocab) return t;
+    oracle_decode_row(format, table + row * row_bytes, cols, out + t * cols);
+  }
+  return -1;
+}
+
 /* kernels/quantize.h:10-25: a wave of 32 lanes holds a block, lane l its
  * value l; amax is the fmaxf of |x| over the lanes, d = amax / 127.0f, the
  * code int(roundf(x / d)) (0 for d == 0), its int8 kept; lane 0 writes d and

@@ -77,6 +77,34 @@ void oracle_wan_angles(int frames, int rows, int cols, int head_dim, double thet
  * of the first id outside [0, vocab) (the reference refuses it), or -1. */
 int64_t oracle_embedding_q8_0(const uint8_t* table, int64_t vocab, int64_t cols, const int32_t* ids, int64_t count,
                               float* out);
+/* ---- storage types by their GGUF type ids (tensor/DType.scala and the
+ * quant objects): decoders restating each decodeBlock in float. ---- */
+enum {
+  ORACLE_F32 = 0,
+  ORACLE_F16 = 1,
+  ORACLE_Q4_0 = 2,
+  ORACLE_Q4_1 = 3,
+  ORACLE_Q5_0 = 6,
+  ORACLE_Q5_1 = 7,
+  ORACLE_Q8_0 = 8,
+  ORACLE_Q4_K = 12,
+  ORACLE_Q5_K = 13,
+  ORACLE_Q6_K = 14,
+  ORACLE_IQ4_NL = 20,
+  ORACLE_IQ4_XS = 23,
+  ORACLE_BF16 = 30,
+  ORACLE_ROCMFP4 = 100,
+  ORACLE_ROCMFP4_FAST = 101
+};
+/* Values and bytes of a block; -1 for an unknown format. */
+int oracle_format_block(int format, int* block_values, int* block_bytes);
+float oracle_rocmfp4_half_scale(int byte);
+/* A row of `cols` values (whole blocks); -1 if not. */
+int oracle_decode_row(int format, const uint8_t* row, int64_t cols, float* out);
+/* ops/CpuLinear.scala:12-41: the first id outside [0, vocab), -1 if none,
+ * -2 for a bad format or partial blocks. */
+int64_t oracle_embedding(int format, const uint8_t* table, int64_t vocab, int64_t cols, const int32_t* ids,
+                         int64_t count, float* out);
 /* ---- F32 tables: ops/CpuLinear.scala:12-41 with DType.F32 ---- */
 int64_t oracle_embedding_f32(const float* table, int64_t vocab, int64_t cols, const int32_t* ids, int64_t count,
                              float* out);

@@ -56,6 +56,10 @@ _F64 = ctypes.c_double
 
 def _declare(l: ctypes.CDLL) -> None:
     sig = {
+        "oracle_format_block": (_I32, [_I32, _P, _P]),
+        "oracle_rocmfp4_half_scale": (_F32, [_I32]),
+        "oracle_decode_row": (_I32, [_I32, _P, _I64, _P]),
+        "oracle_embedding": (_I64, [_I32, _P, _I64, _I64, _P, _I64, _P]),
         "oracle_to_bf16": (ctypes.c_uint16, [_F32]),
         "oracle_from_bf16": (_F32, [ctypes.c_uint16]),
         "oracle_f16_to_f32": (_F32, [ctypes.c_uint16]),
@@ -421,6 +425,78 @@ def embedding_q8_0_bf16(table, vocab, cols, ids):
     """The F32 gather converted to BF16: bit-exact by construction, since the
     product of an fp16 scale and an int8 code is exact in F32."""
     return to_bf16(embedding_q8_0(table, vocab, cols, ids))
+
+
+# ---------------------------------------------------------------- storage types
+
+# GGUF type ids of the storage types with decoders (tensor/DType.scala and the
+# quant objects' ggmlId), and where each block keeps its f16 scales (for
+# the test tables; ROCmFP4 keeps E4M3 scale bytes at 16 and 17 instead).
+FORMATS = {"F32": 0, "F16": 1, "Q4_0": 2, "Q4_1": 3, "Q5_0": 6, "Q5_1": 7, "Q8_0": 8, "Q4_K": 12, "Q5_K": 13,
+           "Q6_K": 14, "IQ4_NL": 20, "IQ4_XS": 23, "BF16": 30, "Q4_0_ROCMFP4": 100, "Q4_0_ROCMFP4_FAST": 101}
+_F16_FIELDS = {"Q4_0": (0,), "Q4_1": (0, 2), "Q5_0": (0,), "Q5_1": (0, 2), "Q8_0": (0,), "Q4_K": (0, 2),
+               "Q5_K": (0, 2), "Q6_K": (208,), "IQ4_NL": (0,), "IQ4_XS": (0,)}
+
+
+def format_block(name: str):
+    """(values, bytes) of a block of storage type `name`."""
+    values, size = ctypes.c_int(), ctypes.c_int()
+    _need(lib().oracle_format_block(FORMATS[name], ctypes.byref(values), ctypes.byref(size)) == 0, name)
+    return values.value, size.value
+
+
+def row_bytes(name: str, cols: int) -> int:
+    values, size = format_block(name)
+    _need(cols % values == 0, f"{cols} values are not whole {name} blocks of {values}")
+    return cols // values * size
+
+
+def rocmfp4_half_scale(byte: int) -> float:
+    return lib().oracle_rocmfp4_half_scale(byte)
+
+
+def decode_row(name: str, row, cols: int) -> np.ndarray:
+    """One row's bytes decoded to F32, as DType.decode (tensor/DType.scala)."""
+    row = _c(row, np.uint8)
+    _need(row.size >= row_bytes(name, cols), f"{row.size} bytes for a {name} row of {cols}")
+    out = np.empty(cols, np.float32)
+    lib().oracle_decode_row(FORMATS[name], _ptr(row), cols, _ptr(out))
+    return out
+
+
+def embedding(name: str, table, vocab: int, cols: int, ids) -> np.ndarray:
+    """CpuLinear.embedding (ops/CpuLinear.scala:12-41): rows `ids` of a table
+    of storage type `name` (its bytes, [vocab, row bytes]), as F32."""
+    table = _c(table, np.uint8)
+    ids = _c(ids, np.int32)
+    _need(table.size >= vocab * row_bytes(name, cols), "table bytes")
+    out = np.empty((ids.size, cols), np.float32)
+    bad = lib().oracle_embedding(FORMATS[name], _ptr(table), vocab, cols, _ptr(ids), ids.size, _ptr(out))
+    _need(bad == -1, f"token id {ids[bad] if bad >= 0 else '?'} outside the table")
+    return out
+
+
+def embedding_bf16(name: str, table, vocab: int, cols: int, ids) -> np.ndarray:
+    return to_bf16(embedding(name, table, vocab, cols, ids))
+
+
+def quant_table(name: str, rows: int, cols: int, rng: np.random.Generator) -> np.ndarray:
+    """Random bytes of a [rows, cols] table of storage type `name` whose
+    values are all finite: f16 scales uniform in +-[1e-3, 2e-2], ROCmFP4 scale
+    bytes finite E4M3 codes, dense values random normals."""
+    if name in ("F32", "F16", "BF16"):
+        x = rng.standard_normal((rows, cols)).astype(np.float32)
+        raw = {"F32": x, "F16": x.astype(np.float16), "BF16": to_bf16(x)}[name]
+        return np.ascontiguousarray(raw).view(np.uint8).reshape(rows, -1)
+    values, size = format_block(name)
+    blocks = cols // values
+    t = rng.integers(0, 256, (rows, blocks, size), dtype=np.uint8)
+    for at in _F16_FIELDS.get(name, ()):
+        d = (rng.uniform(1e-3, 2e-2, (rows, blocks)) * rng.choice([-1, 1], (rows, blocks))).astype(np.float16)
+        t[:, :, at:at + 2] = d.view(np.uint8).reshape(rows, blocks, 2)
+    if name.startswith("Q4_0_ROCMFP4"):
+        t[:, :, 16:] = rng.integers(0, 0x7f, (rows, blocks, size - 16), dtype=np.uint8)
+    return t.reshape(rows, blocks * size)
 
 
 # ---------------------------------------------------------------- attention inputs

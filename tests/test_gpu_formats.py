@@ -1,0 +1,95 @@
+"""The embedding gather and the whole-table decode of every storage type the
+runner's GPU backend reads (kernels/matvec.hip:942-954: Q4_0, Q5_1, Q8_0,
+Q4_K, Q5_K, Q6_K, IQ4_NL, IQ4_XS, ROCmFP4 dual and fast, and the dense F32,
+F16, BF16; plus Q4_1 and Q5_0, which the reference decodes on the CPU), on
+the GPU against the oracle's decoders. Bit-exact: F32 outputs are the
+decoders' float arithmetic, BF16 and F16 its result rounded to nearest even.
+Tables are random blocks with finite scales (NaN scales are out: their NaN
+bits follow the hardware)."""
+
+import numpy as np
+import pytest
+import torch
+
+from drift_amd import _lib
+from drift_amd import ops as d
+from oracle import oracle as o
+from tests.helpers import DEV, assert_bits, dev_i32, host_bits, host_f32, step
+
+pytestmark = pytest.mark.gpu
+
+NAMES = sorted(o.FORMATS)
+
+
+@pytest.fixture(scope="module")
+def hip():
+    return d.HipOps()
+
+
+def table_of(name, vocab, cols, seed):
+    rng = np.random.default_rng(seed)
+    raw = o.quant_table(name, vocab, cols, rng)
+    dev = torch.from_numpy(np.ascontiguousarray(raw)).to(DEV)
+    return raw, d.StoredTable(dev, d.STORAGE_TYPES[name], cols)
+
+
+@pytest.mark.parametrize("name", NAMES)
+@pytest.mark.parametrize("out_type", ["f32", "bf16"])
+def test_embedding_every_storage_type(hip, name, out_type):
+    values = d.STORAGE_TYPES[name].values
+    cols = 512 if values == 256 else 96 if values == 32 else 40
+    vocab = 37
+    raw, table = table_of(name, vocab, cols, 11)
+    ids = np.random.default_rng(12).integers(0, vocab, 53).astype(np.int32)
+    ids[:3] = [0, vocab - 1, 0]
+    step(f"embedding {name} -> {out_type}, rows of {cols}")
+    want = o.embedding(name, raw, vocab, cols, ids)
+    if out_type == "f32":
+        out = torch.empty((ids.size, cols), dtype=torch.float32, device=DEV)
+        hip.embedding(table, dev_i32(ids), out)
+        assert_bits(want.view(np.uint32), host_f32(out).view(np.uint32), what=f"{name} f32")
+    else:
+        out = torch.empty((ids.size, cols), dtype=torch.bfloat16, device=DEV)
+        hip.embedding(table, dev_i32(ids), out)
+        assert_bits(o.to_bf16(want), host_bits(out), what=f"{name} bf16")
+
+
+@pytest.mark.parametrize("name", NAMES)
+@pytest.mark.parametrize("out_type", ["bf16", "f16"])
+def test_dequantize_every_storage_type(hip, name, out_type):
+    values = d.STORAGE_TYPES[name].values
+    cols = 768 if values == 256 else 160 if values == 32 else 64
+    rows = 29
+    raw, table = table_of(name, rows, cols, 21)
+    step(f"dequantize {name} -> {out_type} [{rows}, {cols}]")
+    want = o.embedding(name, raw, rows, cols, np.arange(rows, dtype=np.int32))
+    out = torch.empty((rows, cols), dtype=torch.bfloat16 if out_type == "bf16" else torch.float16, device=DEV)
+    hip.dequantize(table, out)
+    expected = o.to_bf16(want) if out_type == "bf16" else want.astype(np.float16).view(np.uint16)
+    assert_bits(expected, host_bits(out), what=f"{name} dequantize {out_type}")
+
+
+@pytest.mark.parametrize("name", ["Q4_K", "IQ4_NL", "Q4_0_ROCMFP4_FAST"])
+def test_ids_outside_the_table_give_zero_rows(hip, name):
+    values = d.STORAGE_TYPES[name].values
+    cols = 256 if values == 256 else 64
+    raw, table = table_of(name, 5, cols, 3)
+    ids = np.array([1, -1, 5, 4], np.int32)
+    step(f"embedding {name} with ids outside the table")
+    bad = torch.zeros(1, dtype=torch.int32, device=DEV)
+    out = torch.empty((4, cols), dtype=torch.float32, device=DEV)
+    hip.embedding(table, dev_i32(ids), out, bad)
+    got = host_f32(out)
+    want = o.embedding(name, raw, 5, cols, ids[[0, 3]])
+    assert np.array_equal(got[[0, 3]], want) and not got[[1, 2]].any()
+    assert int(bad.item()) == 1
+
+
+def test_misaligned_tables_are_refused(hip):
+    cols = 256
+    flat = torch.zeros(144 * 3 + 4, dtype=torch.uint8, device=DEV)
+    shifted = d.StoredTable(flat[4:].view(3, 144), d.STORAGE_TYPES["Q4_K"], cols)
+    out = torch.empty((1, cols), dtype=torch.float32, device=DEV)
+    step("embedding Q4_K from a table 4 bytes off an 8-byte boundary")
+    with pytest.raises(_lib.HipError, match="8-byte aligned"):
+        hip.embedding(shifted, dev_i32(np.zeros(1, np.int32)), out)
