@@ -72,10 +72,13 @@ SIGNATURES = {
     "drift_embedding_bf16": (_I32, [_P, _I32, _P, _P, _I64, _I64, _I32, _P, _P]),
     "drift_dequantize_bf16": (_I32, [_P, _I32, _P, _I64, _I32, _P]),
     "drift_dequantize_f16": (_I32, [_P, _I32, _P, _I64, _I32, _P]),
+    "drift_rotated_embedding_f32": (_I32, [_P, _P, _I64, _P, _P, _I32, _P, _P, _I64, _I64, _I32, _P, _P]),
+    "drift_rotated_embedding_bf16": (_I32, [_P, _P, _I64, _P, _P, _I32, _P, _P, _I64, _I64, _I32, _P, _P]),
+    "drift_rotated_dequantize_bf16": (_I32, [_P, _P, _I64, _P, _P, _I32, _P, _I64, _I32, _P]),
     "drift_convert": (_I32, [_P, _P, _I64, _I32, _P]),
 }
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 
 class NotBuilt(RuntimeError):

@@ -1,0 +1,337 @@
+// ConvRot's rotated linears, decoded on gfx950 where the file holds their
+// codes: ComfyUI's int8_tensorwise (one int8 a value, a scale a row or one for
+// all) and asym_w4a8_int8 (two 4-bit codes a byte, each a level of a 16-entry
+// codebook times its group's fp8 relative scale, rounded and clamped to int8,
+// times a scale a row), every 256 columns times the normalized regular
+// Hadamard matrix (tensor/ConvRot.scala:20-50). Rows `ids` of one gathered as
+// F32 or BF16 (the embedding, ops/HipLinear.scala:54-92), or the whole weight
+// as BF16 for the GEMM path (ops/HipBase.scala:276-311, the convert of
+// ops/HipMemory.scala:127-130); the reference's kernels are
+// kernels/convrot.hip:84-121.
+//
+// The 256 x 256 matrix is the Kronecker fourth power of a 4 x 4 one, so the
+// rotation is four rounds of 4-point butterflies over the base-4 digits of
+// the column (strides 1, 4, 16, 64), each `half = (a + b + c + d) / 2` summed
+// left to right, then `half - d, half - c, half - b, half - a`: float, in the
+// CPU's order, no contraction, so outputs are the CPU's bit for bit.
+//
+// Layout on the wave: four lanes a group of 256 values, a lane a quarter of
+// it (64 consecutive values, digits 0-2 in its registers, digit 3 its lane
+// in the quad), 16 groups a wave. A lane loads its codes with 16-byte loads
+// (64 B of int8, 32 B of nibbles), decodes, and runs the rounds of digits 0,
+// 1 and 2 in registers. The quad then trades values through the wave's own
+// LDS (4 KiB, a quarter of the values at a time), so that a lane holds digit
+// 3 and digits 0-1 for one digit 2; it runs the last round in registers and
+// stores 16 consecutive outputs per digit 3 (32 B of BF16, 64 B of F32).
+// LDS slots are laid out so that neither the writes nor the reads of a
+// 16-lane phase share a bank.
+#include "common.hpp"
+
+namespace drift {
+namespace {
+
+constexpr int kGroup = 256;       // ConvRot.Group
+constexpr int kLaneValues = 64;   // a quarter group
+constexpr int kWaveGroups = 16;   // 64 lanes, 4 a group
+constexpr int kBlockWaves = 4;
+
+// fp8 E4M3 "fn" (tensor/DType.scala:105-115): bias 7, no infinities, NaN at
+// S.1111.111.
+__device__ __forceinline__ float e4m3(uint32_t code) {
+  const int exponent = (int)((code >> 3) & 0xfu), mantissa = (int)(code & 7u);
+  float magnitude;
+  if (exponent == 0xf && mantissa == 7)
+    magnitude = __builtin_nanf("");
+  else if (exponent == 0)
+    magnitude = ldexpf((float)mantissa, -9);
+  else
+    magnitude = ldexpf((float)(8 + mantissa), exponent - 10);
+  return (code & 0x80u) ? -magnitude : magnitude;
+}
+
+// One butterfly of ConvRot.rotate (tensor/ConvRot.scala:33-42) on v[i],
+// v[i + S], v[i + 2S], v[i + 3S].
+template <int S>
+__device__ __forceinline__ void butterfly(float* v, int i) {
+  const float a = v[i], b = v[i + S], c = v[i + 2 * S], d = v[i + 3 * S];
+  const float half = (((a + b) + c) + d) * 0.5f;
+  v[i] = half - d;
+  v[i + S] = half - c;
+  v[i + 2 * S] = half - b;
+  v[i + 3 * S] = half - a;
+}
+
+// A round over the 64 values of a lane: every butterfly of stride S.
+template <int S>
+__device__ __forceinline__ void round_of(float (&v)[kLaneValues]) {
+#pragma unroll
+  for (int block = 0; block < kLaneValues; block += 4 * S)
+#pragma unroll
+    for (int i = block; i < block + S; ++i) butterfly<S>(v, i);
+}
+
+// The codes of a lane's 64 values: `Bytes` bytes from p, in 16-byte loads
+// where p allows, byte loads where it does not.
+template <int Bytes, bool ALIGNED>
+__device__ __forceinline__ void load_codes(const uint8_t* p, uint32_t (&w)[Bytes / 4]) {
+  if constexpr (ALIGNED) {
+#pragma unroll
+    for (int k = 0; k < Bytes / 16; ++k) {
+      const uint4 q = stream_load(p + 16 * k);
+      w[4 * k] = q.x;
+      w[4 * k + 1] = q.y;
+      w[4 * k + 2] = q.z;
+      w[4 * k + 3] = q.w;
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < Bytes / 4; ++k)
+      w[k] = (uint32_t)p[4 * k] | ((uint32_t)p[4 * k + 1] << 8) | ((uint32_t)p[4 * k + 2] << 16) |
+             ((uint32_t)p[4 * k + 3] << 24);
+  }
+}
+
+// Orders a wave's LDS writes before its lanes' reads of them, and back.
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// 16 consecutive outputs: BF16 (two 16-byte stores), or F32 holding the
+// BF16 value (ops/CpuLinear.scala:24-29; four 16-byte stores).
+__device__ __forceinline__ void store_run(uint16_t* p, const float* v) {
+  Chunk<uint16_t>::store(p, *reinterpret_cast<const float(*)[8]>(v));
+  Chunk<uint16_t>::store(p + 8, *reinterpret_cast<const float(*)[8]>(v + 8));
+}
+
+__device__ __forceinline__ void store_run(float* p, const float* v) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    float r[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r[i] = __uint_as_float(bf16_bits(v[4 * k + i]) << 16);
+    Chunk<float>::store(p + 4 * k, r);
+  }
+}
+
+// A lane's 64 4-bit values from the words of its codes: lane l holds
+// codebook[l % 16] in `entry`, and a value's entry comes from lane `code`
+// (ds_bpermute, no LDS); KEEP_NAN keeps a NaN level as Java's min and max do.
+template <bool KEEP_NAN>
+__device__ __forceinline__ void decode_nibbles(const uint32_t (&w)[8], float entry, const float (&rel)[4], float scale,
+                                               float (&v)[kLaneValues]) {
+#pragma unroll
+  for (int j = 0; j < kLaneValues; ++j) {
+    const int shift = 4 * (j % 8) - 2;  // the code times 4: its lane's byte address
+    const uint32_t word = w[j / 8];
+    const int at = (int)((shift < 0 ? word << 2 : word >> shift) & 0x3cu);
+    const float level =
+        __builtin_rintf(__int_as_float(__builtin_amdgcn_ds_bpermute(at, __float_as_int(entry))) * rel[j / 16]);
+    float clamped = fminf(fmaxf(level, -127.0f), 127.0f);
+    if (KEEP_NAN && level != level) clamped = level;
+    v[j] = clamped * scale;
+  }
+}
+
+// What decodes a rotated weight (ops/ConvRotParts.scala): scales F32, one a
+// row or one for all; with a codebook, the 4-bit levels' codebook (F32
+// [16]), relative scales (fp8 [rows, cols / group_size]) and group_size.
+struct Parts {
+  const uint8_t* codes;
+  const float* scales;
+  int64_t scale_count;
+  const float* codebook;
+  const uint8_t* relative;
+  int group_size;
+};
+
+// Rows ids[t] (row t with no ids) of a rotated weight [rows, cols] into out
+// [count, cols]; T float (the BF16 value widened, as the reference gathers)
+// or uint16_t (BF16). An id outside [0, rows) gets zeros and sets *bad_id.
+template <typename T, bool FOUR_BIT, bool ALIGNED>
+__global__ void __launch_bounds__(kBlockWaves * kWave)
+    rotated_rows(Parts parts, const int32_t* ids, T* out, int64_t count, int64_t rows, int cols, int32_t* bad_id) {
+  __shared__ float4 trade[kBlockWaves][kWaveGroups * 16];  // 4 KiB a wave
+  const int lane = (int)threadIdx.x % kWave, wave = (int)threadIdx.x / kWave;
+  const int g = lane >> 2, q = lane & 3;  // group in the wave, quarter in the group
+  const int per_row = cols / kGroup;
+  const int64_t groups = count * per_row;
+  const int64_t wanted = ((int64_t)blockIdx.x * kBlockWaves + wave) * kWaveGroups + g;
+  const bool live = wanted < groups;
+  const int64_t group = live ? wanted : groups - 1;  // loads stay in bounds, stores are skipped
+  const int64_t t = group / per_row;
+  const int column = (int)(group - t * per_row) * kGroup;
+  int64_t row = ids ? (int64_t)ids[t] : t;
+  const bool bad = row < 0 || row >= rows;
+  if (bad) row = 0;
+  const int first = column + q * kLaneValues;  // this lane's first column
+
+  float v[kLaneValues];
+  const float scale = parts.scales[parts.scale_count == 1 ? 0 : row];
+  if constexpr (!FOUR_BIT) {
+    // ops/CpuBase.scala:47-49: the code as float times the row's scale
+    uint32_t w[16];
+    load_codes<64, ALIGNED>(parts.codes + row * cols + first, w);
+#pragma unroll
+    for (int j = 0; j < kLaneValues; ++j) v[j] = (float)(int8_t)(w[j / 4] >> (8 * (j % 4))) * scale;
+  } else {
+    // ops/CpuBase.scala:50-66: the low nibble the even column; level =
+    // clamp(rint(codebook(code) * relative), -127, 127), a NaN kept (Java's
+    // min and max), times the row's scale.
+    const float entry = parts.codebook[lane & 15];
+    uint32_t w[8];
+    load_codes<32, ALIGNED>(parts.codes + row * (cols / 2) + first / 2, w);
+    const int64_t rel_row = row * (cols / parts.group_size);
+    uint32_t rel_code[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) rel_code[r] = parts.relative[rel_row + (first + 16 * r) / parts.group_size];
+    float rel[4];
+    bool nan = !__builtin_isfinite(entry);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      rel[r] = e4m3(rel_code[r]);
+      nan |= (rel_code[r] & 0x7fu) == 0x7fu;
+    }
+    // codebook * relative is finite unless an entry or a relative scale is
+    // not, and then a wave takes the path that keeps NaNs
+    const bool clean = !__any(nan);
+    if (clean)
+      decode_nibbles<false>(w, entry, rel, scale, v);
+    else
+      decode_nibbles<true>(w, entry, rel, scale, v);
+  }
+
+  // digits 0, 1, 2 (strides 1, 4, 16) in registers
+  round_of<1>(v);
+  round_of<4>(v);
+  round_of<16>(v);
+
+  // Trade within the quad, a value of digit 1 at a time: lane q writes its
+  // four runs of digit 2 (4 values of digit 0 each) and reads back, from the
+  // quad's four lanes (digit 3), the runs of digit 2 = q, into the registers
+  // it wrote from. After it, v[16 * d3 + 4 * d1 + d0] is the value of digits
+  // (d0, d1, q, d3). Slot of (g, d3, d2) in the wave's 256: (g / 4) * 64 +
+  // d2 * 16 + 4 * ((d3 + d2) % 4) + g % 4, so the 16 lanes of a phase write,
+  // and read, 16 different slots.
+  float4* slots = trade[wave] + (g >> 2) * 64 + (g & 3);
+#pragma unroll
+  for (int d1 = 0; d1 < 4; ++d1) {
+#pragma unroll
+    for (int d2 = 0; d2 < 4; ++d2) {
+      const int at = 16 * d2 + 4 * d1;
+      slots[d2 * 16 + 4 * ((q + d2) & 3)] = make_float4(v[at], v[at + 1], v[at + 2], v[at + 3]);
+    }
+    wave_sync();
+#pragma unroll
+    for (int d3 = 0; d3 < 4; ++d3) {
+      const float4 r = slots[q * 16 + 4 * ((d3 + q) & 3)];
+      const int at = 16 * d3 + 4 * d1;
+      v[at] = r.x;
+      v[at + 1] = r.y;
+      v[at + 2] = r.z;
+      v[at + 3] = r.w;
+    }
+    wave_sync();  // every lane's reads are done before the next writes
+  }
+
+  // digit 3 (stride 64 in the group, 16 here)
+  round_of<16>(v);
+
+  if (!live) return;
+  if (bad) {
+#pragma unroll
+    for (int j = 0; j < kLaneValues; ++j) v[j] = 0.0f;
+    if (bad_id) *bad_id = 1;
+  }
+  T* base = out + t * cols + column + q * 16;
+#pragma unroll
+  for (int d3 = 0; d3 < 4; ++d3) store_run(base + 64 * d3, v + 16 * d3);
+}
+
+// ---------------------------------------------------------------- launch layer
+
+// Ops.checkRotated (ops/LinearOps.scala:121-157) on the raw arguments, then
+// the launch: a wave per 16 groups of 256 values, one pass.
+template <typename T>
+int rotated_launch(const char* entry, const Parts& parts, const int32_t* ids, T* out, int64_t count, int64_t rows,
+                   int32_t cols, int32_t* bad_id, void* stream) {
+  clear_error();
+  const bool four_bit = parts.codebook != nullptr;
+  if (count < 0 || rows < 0) return refuse("%s: %lld rows of %lld", entry, (long long)count, (long long)rows);
+  if (cols <= 0 || cols % kGroup != 0) return refuse("%s: rows of %d columns", entry, cols);
+  if (!(parts.scale_count == rows || (parts.scale_count == 1 && !four_bit)))
+    return refuse("%s: %lld scales for %lld rows", entry, (long long)parts.scale_count, (long long)rows);
+  if (four_bit && (parts.group_size <= 0 || parts.group_size % 16 != 0 || cols % parts.group_size != 0))
+    return refuse("%s: %d columns in groups of %d", entry, cols, parts.group_size);
+  if (count == 0) return 0;
+  // an id outside the weight reads row 0 (and writes zeros): there must be one
+  if (rows == 0) return refuse("%s: %lld rows of an empty weight", entry, (long long)count);
+  if (!parts.codes || !parts.scales || !out || (four_bit && !parts.relative))
+    return refuse("%s: null codes, scales, relative scales or out", entry);
+  if (!aligned16(out)) return refuse("%s: out is not 16-byte aligned", entry);
+  if (reinterpret_cast<uintptr_t>(parts.scales) % 4 != 0 || reinterpret_cast<uintptr_t>(parts.codebook) % 4 != 0)
+    return refuse("%s: scales or codebook not 4-byte aligned", entry);
+  const int64_t groups = count * (cols / kGroup);
+  const int64_t waves = (groups + kWaveGroups - 1) / kWaveGroups;
+  const int64_t blocks = (waves + kBlockWaves - 1) / kBlockWaves;
+  if (blocks > kOneShotBlocks) return refuse("%s: %lld groups is too many for one launch", entry, (long long)groups);
+  // 16-byte code loads need every lane's run (64 B, or 32 B of nibbles) on a
+  // 16-byte boundary: the weight's start, and its rows (cols is a multiple of
+  // 256, so they are).
+  const bool aligned = aligned16(parts.codes);
+  const hipStream_t s = (hipStream_t)stream;
+  const dim3 grid((unsigned)blocks), block(kBlockWaves * kWave);
+  if (four_bit) {
+    if (aligned)
+      hipLaunchKernelGGL((rotated_rows<T, true, true>), grid, block, 0, s, parts, ids, out, count, rows, cols, bad_id);
+    else
+      hipLaunchKernelGGL((rotated_rows<T, true, false>), grid, block, 0, s, parts, ids, out, count, rows, cols,
+                         bad_id);
+  } else {
+    if (aligned)
+      hipLaunchKernelGGL((rotated_rows<T, false, true>), grid, block, 0, s, parts, ids, out, count, rows, cols,
+                         bad_id);
+    else
+      hipLaunchKernelGGL((rotated_rows<T, false, false>), grid, block, 0, s, parts, ids, out, count, rows, cols,
+                         bad_id);
+  }
+  return launched(entry);
+}
+
+}  // namespace
+}  // namespace drift
+
+using namespace drift;
+
+extern "C" int drift_rotated_embedding_f32(const void* codes, const float* scales, int64_t scale_count,
+                                           const float* codebook, const uint8_t* relative, int32_t group_size,
+                                           const int32_t* ids, float* out, int64_t count, int64_t rows, int32_t cols,
+                                           int32_t* bad_id, void* stream) {
+  if (!ids && count > 0) {
+    clear_error();
+    return refuse("drift_rotated_embedding_f32: null ids");
+  }
+  const Parts parts{static_cast<const uint8_t*>(codes), scales, scale_count, codebook, relative, group_size};
+  return rotated_launch<float>("drift_rotated_embedding_f32", parts, ids, out, count, rows, cols, bad_id, stream);
+}
+
+extern "C" int drift_rotated_embedding_bf16(const void* codes, const float* scales, int64_t scale_count,
+                                            const float* codebook, const uint8_t* relative, int32_t group_size,
+                                            const int32_t* ids, uint16_t* out, int64_t count, int64_t rows,
+                                            int32_t cols, int32_t* bad_id, void* stream) {
+  if (!ids && count > 0) {
+    clear_error();
+    return refuse("drift_rotated_embedding_bf16: null ids");
+  }
+  const Parts parts{static_cast<const uint8_t*>(codes), scales, scale_count, codebook, relative, group_size};
+  return rotated_launch<uint16_t>("drift_rotated_embedding_bf16", parts, ids, out, count, rows, cols, bad_id, stream);
+}
+
+extern "C" int drift_rotated_dequantize_bf16(const void* codes, const float* scales, int64_t scale_count,
+                                             const float* codebook, const uint8_t* relative, int32_t group_size,
+                                             uint16_t* out, int64_t rows, int32_t cols, void* stream) {
+  const Parts parts{static_cast<const uint8_t*>(codes), scales, scale_count, codebook, relative, group_size};
+  return rotated_launch<uint16_t>("drift_rotated_dequantize_bf16", parts, nullptr, out, rows, rows, cols, nullptr,
+                                  stream);
+}

@@ -178,6 +178,49 @@ def Q8_0Table(data: torch.Tensor, cols: int) -> StoredTable:
 
 
 @dataclass(frozen=True)
+class ConvRotLevels:
+    """What makes an int8 level of a 4-bit code (ops/ConvRotParts.scala:5-13):
+    the 16-level `codebook` (F32 [16]) and each row's `relative` scales (fp8
+    E4M3 [rows, cols / groupSize], as uint8 bytes or float8_e4m3fn), one a
+    `groupSize` columns."""
+    codebook: torch.Tensor
+    relative: torch.Tensor
+    groupSize: int
+
+
+@dataclass(frozen=True)
+class ConvRotParts:
+    """What a rotated linear's codes are decoded with
+    (ops/ConvRotParts.scala:15-17): `scales` F32, one a row (or one for all,
+    without `levels`), and a 4-bit linear's `levels`."""
+    scales: torch.Tensor
+    levels: Optional[ConvRotLevels] = None
+
+
+CONVROT_GROUP = 256  # tensor/ConvRot.scala:13
+
+
+@dataclass(frozen=True)
+class RotatedTable:
+    """A rotated linear [rows, cols] left where the file holds it
+    (ops/LinearOps.scala:21-33 `rotated`): ComfyUI's int8_tensorwise codes
+    (I8 [rows, cols], dtype CONVROT_I8) or asym_w4a8_int8's 4-bit codes (two
+    a byte, [rows, cols / 2], dtype CONVROT_W4A8), seen as the weight they
+    make with `parts` (tensor/ConvRot.scala:52-71)."""
+    codes: torch.Tensor
+    parts: ConvRotParts
+    cols: int
+
+    @property
+    def dtype(self) -> str:
+        return "CONVROT_I8" if self.parts.levels is None else "CONVROT_W4A8"
+
+    @property
+    def shape(self) -> tuple:
+        return (self.codes.shape[0], self.cols)
+
+
+@dataclass(frozen=True)
 class QuantizedValues:
     """`values` F32 values at device address `address` that the launch
     numbered `written` also wrote quantized into `buffer`: codes (int8 per
@@ -214,7 +257,8 @@ def _require(condition: bool, message: str) -> None:
 
 
 def _name(dtype) -> str:
-    return {F32: "F32", BF16: "BF16", F16: "F16", I32: "I32"}.get(dtype, str(dtype))
+    return {F32: "F32", BF16: "BF16", F16: "F16", I32: "I32", torch.int8: "I8", torch.uint8: "U8",
+            torch.float8_e4m3fn: "F8_E4M3"}.get(dtype, str(dtype))
 
 
 def _shape(t) -> str:
@@ -316,6 +360,29 @@ def checkEmbedding(table, ids, out) -> None:
     _require(out.dtype in _FLOAT_TYPES, f"embedding takes F32 or BF16, not {_name(out.dtype)}")
     _require(tuple(out.shape) == (ids.shape[0], shape[-1]),
              f"embedding: out {_shape(out)} for {ids.shape[0]} rows of {shape[-1]}")
+
+
+def checkRotated(codes, parts: ConvRotParts) -> RotatedTable:
+    """Ops.checkRotated (ops/LinearOps.scala:121-157): the weight `codes`
+    make with `parts`."""
+    _require(codes.dtype == torch.int8 and codes.dim() == 2,
+             f"rotated: {_name(codes.dtype)} codes {_shape(codes)}")
+    n = codes.shape[0]
+    k = codes.shape[1] * (1 if parts.levels is None else 2)
+    _require(k % CONVROT_GROUP == 0, f"rotated: rows of {k} columns")
+    scaleCount = parts.scales.numel()
+    _require(parts.scales.dtype == F32 and (scaleCount == n or scaleCount == 1 and parts.levels is None),
+             f"rotated: {scaleCount} {_name(parts.scales.dtype)} scales for {n} rows")
+    l = parts.levels
+    if l is not None:
+        _require(l.groupSize > 0 and l.groupSize % 16 == 0 and k % l.groupSize == 0,
+                 f"rotated: {k} columns in groups of {l.groupSize}")
+        _require(l.codebook.dtype == F32 and l.codebook.numel() == 16,
+                 f"rotated: a codebook {_name(l.codebook.dtype)} {_shape(l.codebook)}")
+        _require(l.relative.dtype in (torch.uint8, torch.float8_e4m3fn) and
+                 tuple(l.relative.shape) == (n, k // l.groupSize),
+                 f"rotated: relative scales {_name(l.relative.dtype)} {_shape(l.relative)}")
+    return RotatedTable(codes, parts, k)
 
 
 def checkPageTable(pageTable, cache: KvCache, positions: int) -> None:
@@ -735,11 +802,16 @@ class HipOps:
 
     # ---------------------------------------------------------------- embedding, convert
 
-    def embedding(self, table: StoredTable, ids, out, badId: Optional[torch.Tensor] = None) -> None:
+    def embedding(self, table, ids, out, badId: Optional[torch.Tensor] = None) -> None:
         """Rows `ids` of a table, decoded (ops/LinearOps.scala:16), into out
-        F32 or BF16. An id outside the table (which the reference refuses)
-        gets a zero row and sets `badId` (int32 [1], device) to 1 when given."""
+        F32 or BF16: a StoredTable, or a RotatedTable as the BF16 it holds
+        (ops/HipLinear.scala:28,54-92). An id outside the table (which the
+        reference refuses) gets a zero row and sets `badId` (int32 [1],
+        device) to 1 when given."""
         checkEmbedding(table, ids, out)
+        if isinstance(table, RotatedTable):
+            self._rotated(f"drift_rotated_embedding_{_suffix(out.dtype)}", table, out, ids, badId)
+            return
         t = self._checkStored("embedding", table)
         _require(table.cols % 8 == 0, f"embedding: rows of {table.cols} values (kernels take multiples of 8)")
         _on_device("embedding", table.data, ids, out)
@@ -751,9 +823,39 @@ class HipOps:
             self._launch(f"drift_embedding_{_suffix(out.dtype)}", _ptr(table.data), t.ggmlId, _ptr(ids), _ptr(out),
                          ids.shape[0], vocab, cols, _ptr(badId))
 
-    def dequantize(self, table: StoredTable, out) -> None:
+    def rotated(self, codes, parts: ConvRotParts) -> RotatedTable:
+        """Ops.rotated (ops/LinearOps.scala:21-33): ComfyUI's rotated linear
+        [N, K] left where the file holds it, `codes` I8 [N, K] or with
+        `parts.levels` the 4-bit codes [N, K / 2], seen as the weight they
+        make with `parts`; `embedding`, `dequantize` and `convert` decode it."""
+        return checkRotated(codes, parts)
+
+    def _rotated(self, entry: str, table: RotatedTable, out, ids=None, badId=None) -> None:
+        table = checkRotated(table.codes, table.parts)
+        p, l = table.parts, table.parts.levels
+        _require(table.codes.is_contiguous() and p.scales.is_contiguous() and
+                 (l is None or l.codebook.is_contiguous() and l.relative.is_contiguous()),
+                 f"{entry}: codes, scales and levels must be contiguous")
+        tensors = [table.codes, p.scales, out] + ([] if l is None else [l.codebook, l.relative]) + \
+            ([] if ids is None else [ids])
+        _on_device(entry, *tensors)
+        rows, cols = table.shape
+        head = (_ptr(table.codes), _ptr(p.scales), p.scales.numel(), None if l is None else _ptr(l.codebook),
+                None if l is None else _ptr(l.relative), 0 if l is None else l.groupSize)
+        if ids is None:
+            self._launch(entry, *head, _ptr(out), rows, cols)
+        else:
+            self._launch(entry, *head, _ptr(ids), _ptr(out), ids.shape[0], rows, cols, _ptr(badId))
+
+    def dequantize(self, table, out) -> None:
         """The whole table decoded into out [rows, cols], BF16 or F16, for
-        the GEMM path (kernels/matvec.hip:801-827 dequantize, dequantize_bf16)."""
+        the GEMM path (kernels/matvec.hip:801-827 dequantize, dequantize_bf16);
+        a RotatedTable to BF16 (ops/HipBase.scala:276-311)."""
+        if isinstance(table, RotatedTable):
+            _require(out.dtype == BF16, f"convert: no conversion from {table.dtype} to {_name(out.dtype)}")
+            _require(tuple(out.shape) == table.shape, f"convert: out {_shape(out)} for {list(table.shape)}")
+            self._rotated("drift_rotated_dequantize_bf16", table, out)
+            return
         t = self._checkStored("dequantize", table)
         _require(out.dtype in (BF16, F16), f"dequantize writes BF16 or F16, not {_name(out.dtype)}")
         _require(tuple(out.shape) == table.shape, f"dequantize: out {_shape(out)} for a table {list(table.shape)}")
@@ -774,7 +876,11 @@ class HipOps:
         return t
 
     def convert(self, x, out) -> None:
-        """ops/MemoryOps.scala:46."""
+        """ops/MemoryOps.scala:46; a rotated linear converts to BF16
+        (ops/HipMemory.scala:127-130)."""
+        if isinstance(x, RotatedTable):
+            self.dequantize(x, out)
+            return
         kind = checkConvert(x, out)
         _on_device("convert", x, out)
         self._launch("drift_convert", _ptr(x), _ptr(out), x.numel(), kind)

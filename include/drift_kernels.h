@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define DRIFT_ABI_VERSION 4
+#define DRIFT_ABI_VERSION 5
 
 /* Activation kinds: src/drift/runner/ops/Activation.scala:6-20. */
 enum {
@@ -369,6 +369,45 @@ int drift_dequantize_bf16(const void* table, int32_t format, uint16_t* out, int6
                           void* stream);
 int drift_dequantize_f16(const void* table, int32_t format, uint16_t* out, int64_t rows, int32_t cols,
                          void* stream);
+
+/* ConvRot's rotated linears read where the file holds them (ComfyUI's
+ * int8_tensorwise and asym_w4a8_int8 under convrot, ops/LinearOps.scala:
+ * 21-33 `rotated`, tensor/ConvRot.scala): a weight [rows, cols] (cols a
+ * multiple of 256) whose every 256 columns are the int8 levels times the
+ * normalized regular Hadamard matrix.
+ * - codebook NULL (int8_tensorwise): codes int8 [rows, cols]; scales F32,
+ *   scale_count = rows (one a row) or 1 (one for all); relative and
+ *   group_size unused.
+ * - codebook F32 [16] (asym_w4a8_int8): codes [rows, cols / 2], two 4-bit
+ *   codes a byte, the even column in the low nibble; a level is
+ *   clamp(rint(codebook[code] * e4m3(relative)), -127, 127) (a NaN stays
+ *   NaN, as the CPU's min and max keep it), relative fp8 E4M3 bytes [rows,
+ *   cols / group_size] (group_size a positive multiple of 16 dividing cols);
+ *   scales F32 [rows], scale_count = rows.
+ * Values are the CPU's bit for bit (ops/CpuBase.scala:40-81): the level
+ * times the row's scale in float, rotated in float in ConvRot.rotate's
+ * order. Codes may lie at any alignment (16-byte aligned ones are read with
+ * 16-byte loads); scales and codebook 4-byte aligned; out 16-byte aligned.
+ *
+ * drift_rotated_embedding_*: rows `ids` into out [count, cols] as the BF16
+ * the weight holds (F32: those BF16 values widened, as
+ * ops/CpuLinear.scala:24-29 gathers). An id outside [0, rows) gets zeros and
+ * sets *bad_id = 1 when `bad_id` is given (the CPU refuses it). Replaces
+ * kernels/convrot.hip:90-94,116-121 convrot_gather_f32_i8/_w4a8
+ * (ops/HipLinear.scala:54-92).
+ * drift_rotated_dequantize_bf16: the whole weight into out [rows, cols]
+ * BF16 for the GEMM path. Replaces kernels/convrot.hip:84-88,109-114
+ * convrot_dequantize_bf16_i8/_w4a8 (ops/HipBase.scala:276-311, the convert
+ * of ops/HipMemory.scala:127-130). */
+int drift_rotated_embedding_f32(const void* codes, const float* scales, int64_t scale_count, const float* codebook,
+                                const uint8_t* relative, int32_t group_size, const int32_t* ids, float* out,
+                                int64_t count, int64_t rows, int32_t cols, int32_t* bad_id, void* stream);
+int drift_rotated_embedding_bf16(const void* codes, const float* scales, int64_t scale_count, const float* codebook,
+                                 const uint8_t* relative, int32_t group_size, const int32_t* ids, uint16_t* out,
+                                 int64_t count, int64_t rows, int32_t cols, int32_t* bad_id, void* stream);
+int drift_rotated_dequantize_bf16(const void* codes, const float* scales, int64_t scale_count, const float* codebook,
+                                  const uint8_t* relative, int32_t group_size, uint16_t* out, int64_t rows,
+                                  int32_t cols, void* stream);
 
 /* ---------------------------------------------------------------- convert
  * Elementwise type conversion of n values (kinds above). Replaces

@@ -660,3 +660,94 @@ void oracle_row_gated_add(float* x, const float* y, const float* gate, int64_t r
       x[i] = (float)((double)x[i] + (double)gate[r] * (double)y[i]);
     }
 }
+
+/* ---- ConvRot's rotated linears ---- */
+
+/* tensor/DType.scala:105-115 F8E4M3 ("fn"): bias 7, no infinities, NaN at
+ * S.1111.111; Math.scalb is exact. */
+float oracle_f8e4m3(int code) {
+  const int exponent = (code >> 3) & 0xf, mantissa = code & 7;
+  float magnitude;
+  if (exponent == 0xf && mantissa == 7)
+    magnitude = NAN;
+  else if (exponent == 0)
+    magnitude = ldexpf((float)mantissa, -9);
+  else
+    magnitude = (float)(8 + mantissa) * ldexpf(1.0f, exponent - 10);
+  return (code & 0x80) ? -magnitude : magnitude;
+}
+
+/* tensor/ConvRot.scala:20-50 rotate: each `group` values from `from` times
+ * the normalized regular Hadamard matrix, as rounds of four-point
+ * butterflies over strides 1, 4, 16, ... below `group`, in float: half =
+ * (a + b + c + d) * 0.5 summed left to right, then half - d, half - c,
+ * half - b, half - a. */
+void oracle_convrot_rotate(float* values, int64_t length, int64_t group) {
+  for (int64_t start = 0; start < length; start += group)
+    for (int64_t stride = 1; stride < group; stride *= 4)
+      for (int64_t block = start; block < start + group; block += 4 * stride)
+        for (int64_t i = block; i < block + stride; ++i) {
+          const float a = values[i], b = values[i + stride], c = values[i + 2 * stride], d = values[i + 3 * stride];
+          const float half = (a + b + c + d) * 0.5f;
+          values[i] = half - d;
+          values[i + stride] = half - c;
+          values[i + 2 * stride] = half - b;
+          values[i + 3 * stride] = half - a;
+        }
+}
+
+/* ops/CpuBase.scala:40-81 rotatedRows before its rotation: rows [first,
+ * first + count) of a rotated linear [rows, cols] as the int8 levels times
+ * their row's scale. int8_tensorwise (codebook NULL): codes int8 [rows,
+ * cols], scales one a row or one for all. asym_w4a8_int8: codes two 4-bit
+ * a byte [rows, cols / 2] (the even column the low nibble); the level is
+ * max(-127, min(127, rint(codebook[code] * relative))) in double with
+ * Java's NaN-keeping min and max, relative the row's fp8 scale of the
+ * column's group of group_size. */
+void oracle_convrot_levels(const uint8_t* codes, const float* scales, int64_t scale_count, const float* codebook,
+                           const uint8_t* relative, int64_t group_size, int64_t cols, int64_t first, int64_t count,
+                           float* out) {
+  for (int64_t r = 0; r < count; ++r) {
+    const int64_t row = first + r;
+    const float scale = scales[scale_count == 1 ? 0 : row];
+    for (int64_t c = 0; c < cols; ++c) {
+      float level;
+      if (!codebook) {
+        level = (float)(int8_t)codes[row * cols + c];
+      } else {
+        const uint8_t byte = codes[row * (cols / 2) + c / 2];
+        const int code = (c % 2 == 0) ? (byte & 0xf) : ((byte >> 4) & 0xf);
+        const float rel = oracle_f8e4m3(relative[row * (cols / group_size) + c / group_size]);
+        const double rounded = rint((double)(codebook[code] * rel));
+        const double low = rounded != rounded ? rounded : (127.0 < rounded ? 127.0 : rounded);
+        level = (float)(low != low ? low : (-127.0 > low ? -127.0 : low));
+      }
+      out[r * cols + c] = level * scale;
+    }
+  }
+}
+
+/* ops/CpuBase.scala:40-81 rotatedRows: the levels above, every 256 columns
+ * rotated (ConvRot.Group). */
+void oracle_convrot_rows(const uint8_t* codes, const float* scales, int64_t scale_count, const float* codebook,
+                         const uint8_t* relative, int64_t group_size, int64_t cols, int64_t first, int64_t count,
+                         float* out) {
+  oracle_convrot_levels(codes, scales, scale_count, codebook, relative, group_size, cols, first, count, out);
+  oracle_convrot_rotate(out, count * cols, 256);
+}
+
+/* ops/CpuLinear.scala:12-41 for a rotated table: row ids[t] of the weight
+ * [rows, cols] as the BF16 it holds, widened to F32. Returns the first id
+ * outside [0, rows), -1 if none. */
+int64_t oracle_convrot_embedding(const uint8_t* codes, const float* scales, int64_t scale_count,
+                                 const float* codebook, const uint8_t* relative, int64_t group_size, int64_t rows,
+                                 int64_t cols, const int32_t* ids, int64_t count, float* out) {
+  for (int64_t t = 0; t < count; ++t) {
+    const int64_t row = ids[t];
+    if (row < 0 || row >= rows) return t;
+    float* target = out + t * cols;
+    oracle_convrot_rows(codes, scales, scale_count, codebook, relative, group_size, cols, row, 1, target);
+    for (int64_t c = 0; c < cols; ++c) target[c] = oracle_from_bf16(oracle_to_bf16(target[c]));
+  }
+  return -1;
+}

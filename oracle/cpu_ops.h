@@ -129,6 +129,21 @@ void oracle_row_gated_add(float* x, const float* y, const float* gate, int64_t r
  * the quotient is NaN), xs[b] = xd[b] * (float) sum of the block's codes. */
 void oracle_quantize_x(const float* x, int8_t* xq, float* xd, float* xs, int64_t blocks);
 
+/* ---- ConvRot's rotated linears: tensor/ConvRot.scala, ops/CpuBase.scala:40-81 ---- */
+float oracle_f8e4m3(int code);
+void oracle_convrot_rotate(float* values, int64_t length, int64_t group);
+/* codebook NULL: int8 codes [rows, cols]; else 4-bit codes [rows, cols / 2]
+ * with relative fp8 [rows, cols / group_size]. */
+void oracle_convrot_levels(const uint8_t* codes, const float* scales, int64_t scale_count, const float* codebook,
+                           const uint8_t* relative, int64_t group_size, int64_t cols, int64_t first, int64_t count,
+                           float* out);
+void oracle_convrot_rows(const uint8_t* codes, const float* scales, int64_t scale_count, const float* codebook,
+                         const uint8_t* relative, int64_t group_size, int64_t cols, int64_t first, int64_t count,
+                         float* out);
+int64_t oracle_convrot_embedding(const uint8_t* codes, const float* scales, int64_t scale_count,
+                                 const float* codebook, const uint8_t* relative, int64_t group_size, int64_t rows,
+                                 int64_t cols, const int32_t* ids, int64_t count, float* out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -87,6 +87,11 @@ def _declare(l: ctypes.CDLL) -> None:
         "oracle_modulate_chunks": (None, [_P, _P, _P, _I64, _I64, _I64, _I64, _I64]),
         "oracle_gated_add_chunk": (None, [_P, _P, _P, _I64, _I64, _I64, _I64]),
         "oracle_row_gated_add": (None, [_P, _P, _P, _I64, _I64]),
+        "oracle_f8e4m3": (_F32, [_I32]),
+        "oracle_convrot_rotate": (None, [_P, _I64, _I64]),
+        "oracle_convrot_levels": (None, [_P, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _P]),
+        "oracle_convrot_rows": (None, [_P, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _P]),
+        "oracle_convrot_embedding": (_I64, [_P, _P, _I64, _P, _P, _I64, _I64, _I64, _P, _I64, _P]),
     }
     for name, (restype, argtypes) in sig.items():
         fn = getattr(l, name)
@@ -612,3 +617,92 @@ def q8_0_table(rows: int, cols: int, rng: np.random.Generator, scale_lo=1e-3, sc
     raw[:, 0:2] = scales.view(np.uint8).reshape(blocks, 2)
     raw[:, 2:] = rng.integers(-127, 128, (blocks, 32)).astype(np.int8).view(np.uint8)
     return raw.reshape(rows, cols // 32 * 34)
+
+
+# ---------------------------------------------------------------- ConvRot rotated linears
+
+CONVROT_GROUP = 256  # tensor/ConvRot.scala:13
+
+
+def f8e4m3(code: int) -> float:
+    """DType.F8E4M3 (tensor/DType.scala:105-115)."""
+    return lib().oracle_f8e4m3(int(code))
+
+
+def convrot_rotate(values, group: int = CONVROT_GROUP) -> np.ndarray:
+    """ConvRot.rotate (tensor/ConvRot.scala:20-50) of a copy of `values`,
+    every `group` of them."""
+    out = _c(values, np.float32).copy()
+    _need(out.size % group == 0, f"{out.size} values are not whole groups of {group}")
+    lib().oracle_convrot_rotate(_ptr(out), out.size, group)
+    return out.reshape(np.shape(values))
+
+
+class Rotated:
+    """A rotated linear [rows, cols] as a file holds it (ops/LinearOps.scala:
+    21-33, ops/ConvRotParts.scala): `codes` uint8 [rows, cols] (int8
+    codes) or [rows, cols / 2] (4-bit, with `codebook` F32 [16], `relative`
+    fp8 bytes [rows, cols / group_size] and `group_size`), and `scales` F32
+    [rows] (or [1] for int8 codes)."""
+
+    def __init__(self, codes, scales, cols, codebook=None, relative=None, group_size=0):
+        self.codes = _c(codes, np.uint8)
+        self.scales = _c(scales, np.float32)
+        self.cols, self.group_size = int(cols), int(group_size)
+        self.codebook = None if codebook is None else _c(codebook, np.float32)
+        self.relative = None if relative is None else _c(relative, np.uint8)
+        self.rows = self.codes.shape[0]
+        per_row = self.cols // 2 if self.codebook is not None else self.cols
+        _need(self.codes.size == self.rows * per_row, "codes")
+        if self.codebook is not None:
+            _need(self.codebook.size == 16 and self.group_size > 0 and self.cols % self.group_size == 0, "levels")
+            _need(self.relative.size == self.rows * (self.cols // self.group_size), "relative scales")
+
+    def _args(self):
+        return (_ptr(self.codes), _ptr(self.scales), self.scales.size, _ptr(self.codebook), _ptr(self.relative),
+                self.group_size, self.cols)
+
+    def levels(self, first: int = 0, count: int | None = None) -> np.ndarray:
+        """The rows' values before their rotation (int8 level times scale)."""
+        count = self.rows - first if count is None else count
+        out = np.empty((count, self.cols), np.float32)
+        lib().oracle_convrot_levels(*self._args(), first, count, _ptr(out))
+        return out
+
+    def rows_of(self, first: int = 0, count: int | None = None) -> np.ndarray:
+        """CpuBase.rotatedRows (ops/CpuBase.scala:40-81): the F32 weight rows."""
+        _need(self.cols % CONVROT_GROUP == 0, f"rotated: rows of {self.cols} columns")
+        count = self.rows - first if count is None else count
+        out = np.empty((count, self.cols), np.float32)
+        lib().oracle_convrot_rows(*self._args(), first, count, _ptr(out))
+        return out
+
+    def embedding(self, ids) -> np.ndarray:
+        """CpuLinear.embedding of a rotated table (ops/CpuLinear.scala:12-41):
+        rows `ids` as the BF16 they hold, widened to F32."""
+        ids = _c(ids, np.int32)
+        out = np.empty((ids.size, self.cols), np.float32)
+        bad = lib().oracle_convrot_embedding(*self._args()[:6], self.rows, self.cols, _ptr(ids), ids.size, _ptr(out))
+        _need(bad == -1, f"token id {ids[bad] if bad >= 0 else '?'} outside the table")
+        return out
+
+    def dequantize_bf16(self) -> np.ndarray:
+        """convert to BF16 (ops/HipMemory.scala:127-130): the rows rounded."""
+        return to_bf16(self.rows_of())
+
+
+def random_rotated(rows: int, cols: int, rng: np.random.Generator, four_bit: bool = False, group_size: int = 32,
+                   one_scale: bool = False) -> Rotated:
+    """A random rotated weight: int8 codes in [-128, 127] with scales uniform
+    in [1e-4, 1e-2]; or 4-bit codes with a sorted codebook uniform in [-1, 1],
+    positive relative scales 0x58..0x76 (16 to 240, so the int8 clamp is
+    exercised) and row scales in [1e-4, 1e-3]."""
+    if not four_bit:
+        codes = rng.integers(0, 256, (rows, cols), dtype=np.uint8)
+        scales = rng.uniform(1e-4, 1e-2, 1 if one_scale else rows).astype(np.float32)
+        return Rotated(codes, scales, cols)
+    codes = rng.integers(0, 256, (rows, cols // 2), dtype=np.uint8)
+    codebook = np.sort(rng.uniform(-1, 1, 16)).astype(np.float32)
+    relative = rng.integers(0x58, 0x77, (rows, cols // group_size), dtype=np.uint8)
+    scales = rng.uniform(1e-4, 1e-3, rows).astype(np.float32)
+    return Rotated(codes, scales, cols, codebook, relative, group_size)

@@ -23,7 +23,7 @@ def test_header_and_library_agree(lib):
 
 
 def test_version_and_error_text(lib):
-    assert lib.drift_abi_version() == _lib.ABI_VERSION == 4
+    assert lib.drift_abi_version() == _lib.ABI_VERSION == 5
     assert lib.drift_error_string(0).decode().lower().startswith("no error")
     assert lib.drift_error_string(1)
 
@@ -128,3 +128,26 @@ def test_attention_inputs_refuse_what_the_cache_checks_refuse(lib):
     assert "multiple of 16" in refused(lib, "drift_attention_inputs_f32", *ai(16, 2, 256, 64, 8, 4, 14))
     assert "page table" in refused(lib, "drift_attention_inputs_f32", *ai(16, 2, 256, 64, 16, 1, 14))
     assert "key heads" in refused(lib, "drift_attention_inputs_bf16", *ai(16, -2, 256, 64, 16, 4, 14))
+
+
+def test_rotated_tables_refuse_what_checkRotated_refuses(lib):
+    p, out = ctypes.c_void_p(16), ctypes.c_void_p(256)
+    book = ctypes.c_void_p(64)
+    ids = ctypes.c_void_p(128)
+    assert "rows of 200 columns" in refused(lib, "drift_rotated_dequantize_bf16", p, p, 4, NULL, NULL, 0, out, 4,
+                                            200, NULL)
+    assert "3 scales for 4 rows" in refused(lib, "drift_rotated_dequantize_bf16", p, p, 3, NULL, NULL, 0, out, 4,
+                                            256, NULL)
+    # one scale for all is int8's only: 4-bit weights take one a row
+    assert "1 scales for 4 rows" in refused(lib, "drift_rotated_dequantize_bf16", p, p, 1, book, p, 32, out, 4,
+                                            256, NULL)
+    assert "256 columns in groups of 24" in refused(lib, "drift_rotated_dequantize_bf16", p, p, 4, book, p, 24, out,
+                                                    4, 256, NULL)
+    assert "null codes" in refused(lib, "drift_rotated_dequantize_bf16", p, p, 4, book, NULL, 32, out, 4, 256, NULL)
+    assert "16-byte aligned" in refused(lib, "drift_rotated_embedding_bf16", p, p, 4, NULL, NULL, 0, ids,
+                                        ctypes.c_void_p(8), 3, 4, 256, NULL, NULL)
+    assert "empty weight" in refused(lib, "drift_rotated_embedding_f32", p, p, 0, NULL, NULL, 0, ids, out, 3, 0,
+                                     256, NULL, NULL)
+    assert "null ids" in refused(lib, "drift_rotated_embedding_f32", p, p, 4, NULL, NULL, 0, NULL, out, 3, 4, 256,
+                                 NULL, NULL)
+    assert lib.drift_rotated_embedding_bf16(NULL, NULL, 4, NULL, NULL, 0, NULL, NULL, 0, 4, 256, NULL, NULL) == 0

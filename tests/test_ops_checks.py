@@ -153,3 +153,35 @@ def test_split_halves_and_attention_inputs_are_checked(hip):
                             f32(t, heads, 8), f32(t, heads, 8), f32(t, 2, 8), f32(t, heads, 8))
     with pytest.raises(ValueError, match="tensors live in device memory"):
         hip.attentionInputs(*args(f32(t, heads, 16), f32(t, heads, 8)))
+
+
+def test_rotated_weights_are_checked_as_checkRotated_does(hip):
+    codes = torch.zeros((4, 256), dtype=torch.int8)
+    scales = torch.ones(4)
+    t = hip.rotated(codes, d.ConvRotParts(scales))
+    assert t.shape == (4, 256) and t.dtype == "CONVROT_I8"
+    assert hip.rotated(codes, d.ConvRotParts(torch.ones(1))).shape == (4, 256)
+    with pytest.raises(ValueError, match=r"rotated: U8 codes \[4, 256\]"):
+        hip.rotated(codes.view(torch.uint8), d.ConvRotParts(scales))
+    with pytest.raises(ValueError, match="rotated: rows of 200 columns"):
+        hip.rotated(torch.zeros((4, 200), dtype=torch.int8), d.ConvRotParts(scales))
+    with pytest.raises(ValueError, match="rotated: 3 F32 scales for 4 rows"):
+        hip.rotated(codes, d.ConvRotParts(torch.ones(3)))
+    levels = d.ConvRotLevels(torch.zeros(16), torch.zeros((4, 16), dtype=torch.uint8), 32)
+    four = hip.rotated(torch.zeros((4, 256), dtype=torch.int8), d.ConvRotParts(scales, levels))
+    assert four.shape == (4, 512) and four.dtype == "CONVROT_W4A8"
+    with pytest.raises(ValueError, match="rotated: 1 F32 scales for 4 rows"):
+        hip.rotated(torch.zeros((4, 256), dtype=torch.int8), d.ConvRotParts(torch.ones(1), levels))
+    with pytest.raises(ValueError, match="rotated: 512 columns in groups of 24"):
+        hip.rotated(torch.zeros((4, 256), dtype=torch.int8), d.ConvRotParts(scales, d.ConvRotLevels(
+            torch.zeros(16), torch.zeros((4, 16), dtype=torch.uint8), 24)))
+    with pytest.raises(ValueError, match=r"rotated: a codebook F32 \[8\]"):
+        hip.rotated(torch.zeros((4, 256), dtype=torch.int8), d.ConvRotParts(scales, d.ConvRotLevels(
+            torch.zeros(8), torch.zeros((4, 16), dtype=torch.uint8), 32)))
+    with pytest.raises(ValueError, match=r"rotated: relative scales U8 \[4, 8\]"):
+        hip.rotated(torch.zeros((4, 256), dtype=torch.int8), d.ConvRotParts(scales, d.ConvRotLevels(
+            torch.zeros(16), torch.zeros((4, 8), dtype=torch.uint8), 32)))
+    with pytest.raises(ValueError, match="embedding: out \\[3, 256\\] for 2 rows of 256"):
+        hip.embedding(t, torch.zeros(2, dtype=torch.int32), torch.empty((3, 256)))
+    with pytest.raises(ValueError, match="convert: no conversion from CONVROT_I8 to F32"):
+        hip.convert(t, torch.empty((4, 256)))
