@@ -11,6 +11,8 @@ A step is one pass of the path over its configurations, every kernel once:
       Q [65520, 24, 128] on the 21 x 30 x 52 grid; the gated residual with
       per-sample gates, per-row modulation and gated residual from a
       [65520, 6 x 3072] F32 table, and a per-head gate over [65520 x 24, 128]
+  Weights decoded to bf16 for the GEMM path: a Q4_K GGUF weight [14336, 4096],
+      and ComfyUI's rotated linears (ConvRot, int8 and 4-bit codes) [13824, 5120]
 Inputs are synthetic (seeded device generators) and resident in HBM. Each
 kernel rotates through buffer sets totalling more than 512 MB, so the 256 MB
 Infinity Cache cannot hold what the next launch reads.
@@ -283,6 +285,45 @@ def make_kernels(hip: d.HipOps):
     kernels.append(Kernel("row_gated_add_bf16", "per-head gate x[r] += g[r] * y[r] bf16 [65520*24,128]", nbytes, heads,
                           lambda i, n=n: hip.rowGatedAdd(qs5[i % n].view(heads, 128), rq5[i % n].view(heads, 128),
                                                          head_gates), sets=n))
+
+    # Weights decoded for the GEMM path: a Q4_K GGUF weight [14336, 4096] to
+    # bf16, and ComfyUI's rotated linears (int8 codes, and 4-bit codes with
+    # fp8 scales a 64 columns) of a DiT FFN [13824, 5120] to bf16
+    rows_k, cols_k = 14336, 4096
+    nbytes = rows_k * cols_k // 256 * 144 + rows_k * cols_k * 2
+    n = sets_for(nbytes)
+    q4k = []
+    for i in range(n):
+        raw = torch.randint(0, 256, (rows_k, cols_k // 256, 144), generator=gen(1000 + i), device=DEV,
+                            dtype=torch.int32).to(torch.uint8)
+        dm = (1e-3 + 1e-2 * torch.rand((rows_k, cols_k // 256, 2), generator=gen(1100 + i), device=DEV)).half()
+        raw[:, :, 0:4] = dm.view(torch.uint8).view(rows_k, cols_k // 256, 4)
+        q4k.append(d.StoredTable(raw.view(rows_k, -1), d.STORAGE_TYPES["Q4_K"], cols_k))
+    kouts = [torch.empty((rows_k, cols_k), dtype=torch.bfloat16, device=DEV) for _ in range(n)]
+    kernels.append(Kernel("dequantize_q4_k_bf16", "Q4_K weight [14336,4096] decoded to bf16", nbytes, rows_k,
+                          lambda i, n=n: hip.dequantize(q4k[i % n], kouts[i % n]), sets=n))
+    rows_r, cols_r, group = 13824, 5120, 64
+    for four in (False, True):
+        code_bytes = rows_r * cols_r // (2 if four else 1)
+        nbytes = code_bytes + rows_r * 4 + rows_r * cols_r * 2 + (rows_r * cols_r // group if four else 0)
+        n = sets_for(nbytes)
+        weights = []
+        for i in range(n):
+            codes = torch.randint(-128, 128, (rows_r, cols_r // (2 if four else 1)), generator=gen(1200 + i),
+                                  device=DEV, dtype=torch.int32).to(torch.int8)
+            scales = (1e-4 + 1e-3 * torch.rand(rows_r, generator=gen(1300 + i), device=DEV)).float()
+            levels = None
+            if four:
+                book = torch.sort(2 * torch.rand(16, generator=gen(1400 + i), device=DEV) - 1).values.float()
+                rel = torch.randint(0x58, 0x77, (rows_r, cols_r // group), generator=gen(1500 + i), device=DEV,
+                                    dtype=torch.int32).to(torch.uint8)
+                levels = d.ConvRotLevels(book, rel, group)
+            weights.append(hip.rotated(codes, d.ConvRotParts(scales, levels)))
+        routs = [torch.empty((rows_r, cols_r), dtype=torch.bfloat16, device=DEV) for _ in range(n)]
+        name = "rotated_dequantize_w4a8_bf16" if four else "rotated_dequantize_i8_bf16"
+        what = "4-bit (fp8 scales a 64 columns)" if four else "int8"
+        kernels.append(Kernel(name, f"ConvRot rotated linear, {what} codes [13824,5120] decoded to bf16", nbytes,
+                              rows_r, lambda i, n=n, w=weights, o_=routs: hip.convert(w[i % n], o_[i % n]), sets=n))
     return kernels
 
 
@@ -396,6 +437,18 @@ def cpu_baseline(kernels, budget_s: float):
         c, s = cos[index], sin[index]
         return lambda: o.to_bf16(o.rope_table(x, c, s))
 
+    q4k_table = o.quant_table("Q4_K", 64, 4096, rng)
+
+    def dequantize_q4_k(units):
+        table = np.concatenate([q4k_table] * math.ceil(units / 64))[:units]
+        return lambda: o.embedding_bf16("Q4_K", table, units, 4096, np.arange(units, dtype=np.int32))
+
+    def rotated(four):
+        def make(units):
+            r = o.random_rotated(units, 5120, rng, four, 64)
+            return lambda: r.dequantize_bf16()
+        return make
+
     work = {}
     for b in (1, 8, 64):
         work[f"rms_norm_bf16_b{b}"] = (rms, b, "rows")
@@ -409,7 +462,10 @@ def cpu_baseline(kernels, budget_s: float):
                  "rope_3d_bf16": (rope3d, 65520, "tokens"), "gated_add_bf16": (gated_add, 65520, "rows"),
                  "modulate_chunks_bf16": (modulate_chunks, 65520, "rows"),
                  "gated_add_chunk_bf16": (gated_add_chunk, 65520, "rows"),
-                 "row_gated_add_bf16": (row_gated_add, 65520 * 24, "head rows")})
+                 "row_gated_add_bf16": (row_gated_add, 65520 * 24, "head rows"),
+                 "dequantize_q4_k_bf16": (dequantize_q4_k, 14336, "rows"),
+                 "rotated_dequantize_i8_bf16": (rotated(False), 13824, "rows"),
+                 "rotated_dequantize_w4a8_bf16": (rotated(True), 13824, "rows")})
     # Each kernel gets 2/3 of budget_s / (kernels) seconds on one core: a sample of
     # up to the whole launch's units, run once untimed and then again until
     # that time is spent; the per-run time is what scales to the whole
@@ -554,8 +610,9 @@ def main():
         "data": "synthetic (seeded device generators), resident in HBM; buffer sets rotated past the 256 MB MALL",
         "config": {
             "workload": "drift fused layer kernels, one pass over C2 (decode B=1,8,64; F32 with int8 side output "
-                        "B=1,64), C3 (prefill QK norm+RoPE), C4 (Q8_0 gather), C5 (Video DiT AdaLN, GELU-tanh, "
-                        "3-D RoPE, gated residuals, per-row modulation)",
+                        "B=1,64), C3 (prefill QK norm+RoPE, and with the paged KV-cache write), C4 (Q8_0 gather), "
+                        "C5 (Video DiT AdaLN, GELU-tanh, 3-D RoPE, gated residuals, per-row modulation), and "
+                        "weights decoded to bf16 (Q4_K [14336,4096]; ConvRot int8 and 4-bit [13824,5120])",
             "step_bytes": step_bytes,
             "parallelism": "single GPU",
         },
