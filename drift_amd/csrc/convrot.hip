@@ -22,9 +22,10 @@
 // 1 and 2 in registers. The quad then trades values through the wave's own
 // LDS (4 KiB, a quarter of the values at a time), so that a lane holds digit
 // 3 and digits 0-1 for one digit 2; it runs the last round in registers and
-// stores 16 consecutive outputs per digit 3 (32 B of BF16, 64 B of F32).
-// LDS slots are laid out so that neither the writes nor the reads of a
-// 16-lane phase share a bank.
+// passes its outputs back through the LDS so that every store instruction
+// writes whole 128-byte lines (half-line stores had the L2 write 1.5 times
+// the output to HBM). The trade's LDS slots are laid out so that neither the
+// writes nor the reads of a 16-lane phase share a bank.
 #include "common.hpp"
 
 namespace drift {
@@ -98,21 +99,21 @@ __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// 16 consecutive outputs: BF16 (two 16-byte stores), or F32 holding the
-// BF16 value (ops/CpuLinear.scala:24-29; four 16-byte stores).
-__device__ __forceinline__ void store_run(uint16_t* p, const float* v) {
-  Chunk<uint16_t>::store(p, *reinterpret_cast<const float(*)[8]>(v));
-  Chunk<uint16_t>::store(p + 8, *reinterpret_cast<const float(*)[8]>(v + 8));
+// 16 consecutive outputs as out holds them, into LDS: BF16 (32 bytes), or
+// F32 holding the BF16 value (ops/CpuLinear.scala:24-29; 64 bytes).
+__device__ __forceinline__ void stage_run(uint8_t* p, const float* v, uint16_t) {
+  uint4* q = reinterpret_cast<uint4*>(p);
+  q[0] = make_uint4(pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]), pack_bf16(v[4], v[5]), pack_bf16(v[6], v[7]));
+  q[1] = make_uint4(pack_bf16(v[8], v[9]), pack_bf16(v[10], v[11]), pack_bf16(v[12], v[13]),
+                    pack_bf16(v[14], v[15]));
 }
 
-__device__ __forceinline__ void store_run(float* p, const float* v) {
+__device__ __forceinline__ void stage_run(uint8_t* p, const float* v, float) {
+  uint4* q = reinterpret_cast<uint4*>(p);
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    float r[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) r[i] = __uint_as_float(bf16_bits(v[4 * k + i]) << 16);
-    Chunk<float>::store(p + 4 * k, r);
-  }
+  for (int k = 0; k < 4; ++k)
+    q[k] = make_uint4(bf16_bits(v[4 * k]) << 16, bf16_bits(v[4 * k + 1]) << 16, bf16_bits(v[4 * k + 2]) << 16,
+                      bf16_bits(v[4 * k + 3]) << 16);
 }
 
 // A lane's 64 4-bit values from the words of its codes: lane l holds
@@ -238,15 +239,39 @@ __global__ void __launch_bounds__(kBlockWaves * kWave)
   // digit 3 (stride 64 in the group, 16 here)
   round_of<16>(v);
 
-  if (!live) return;
   if (bad) {
 #pragma unroll
     for (int j = 0; j < kLaneValues; ++j) v[j] = 0.0f;
-    if (bad_id) *bad_id = 1;
+    if (bad_id && live) *bad_id = 1;
   }
-  T* base = out + t * cols + column + q * 16;
+
+  // Out through the wave's LDS, a part at a time (4 KiB: a quarter or half
+  // of each of its 16 groups): the lanes write their runs of the part, then
+  // read it back so that each store instruction's 64 lanes write 16
+  // consecutive 16-byte pieces of four groups, whole 128-byte lines. The
+  // wave's groups are consecutive in out.
+  constexpr int kRunsPerPart = 256 / (4 * 16 * (int)sizeof(T));  // a lane's digit-3 runs in a part: 2 BF16, 1 F32
+  static_assert(kRunsPerPart >= 1 && 4 % kRunsPerPart == 0, "a part is whole runs");
+  uint8_t* part = reinterpret_cast<uint8_t*>(trade[wave]);
+  const int64_t wave_first = ((int64_t)blockIdx.x * kBlockWaves + wave) * kWaveGroups;
 #pragma unroll
-  for (int d3 = 0; d3 < 4; ++d3) store_run(base + 64 * d3, v + 16 * d3);
+  for (int first3 = 0; first3 < 4; first3 += kRunsPerPart) {
+#pragma unroll
+    for (int r = 0; r < kRunsPerPart; ++r)
+      stage_run(part + g * 256 + (r * 64 + q * 16) * (int)sizeof(T), v + 16 * (first3 + r), T{});
+    wave_sync();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int piece = lane + 64 * i;  // 16-byte piece of the part
+      const int pg = piece / 16;        // its group in the wave
+      const uint4 w = reinterpret_cast<const uint4*>(part)[piece];
+      if (wave_first + pg < groups) {
+        T* at = out + (wave_first + pg) * kGroup + first3 * 64 + (piece % 16) * (16 / (int)sizeof(T));
+        __builtin_nontemporal_store(u32x4{w.x, w.y, w.z, w.w}, reinterpret_cast<u32x4*>(at));
+      }
+    }
+    wave_sync();  // the part's reads are done before the next part's writes
+  }
 }
 
 // ---------------------------------------------------------------- launch layer
