@@ -118,21 +118,33 @@ __device__ __forceinline__ void stage_run(uint8_t* p, const float* v, float) {
 
 // A lane's 64 4-bit values from the words of its codes: lane l holds
 // codebook[l % 16] in `entry`, and a value's entry comes from lane `code`
-// (ds_bpermute, no LDS); KEEP_NAN keeps a NaN level as Java's min and max do.
-template <bool KEEP_NAN>
+// (ds_bpermute, no LDS).
+__device__ __forceinline__ int nibble_address(const uint32_t (&w)[8], int j) {
+  const int shift = 4 * (j % 8) - 2;  // the code times 4: its lane's byte address
+  const uint32_t word = w[j / 8];
+  return (int)((shift < 0 ? word << 2 : word >> shift) & 0x3cu);
+}
+
+__device__ __forceinline__ float codebook_times(const uint32_t (&w)[8], float entry, const float (&rel)[4], int j) {
+  return __int_as_float(__builtin_amdgcn_ds_bpermute(nibble_address(w, j), __float_as_int(entry))) * rel[j / 16];
+}
+
 __device__ __forceinline__ void decode_nibbles(const uint32_t (&w)[8], float entry, const float (&rel)[4], float scale,
                                                float (&v)[kLaneValues]) {
 #pragma unroll
-  for (int j = 0; j < kLaneValues; ++j) {
-    const int shift = 4 * (j % 8) - 2;  // the code times 4: its lane's byte address
-    const uint32_t word = w[j / 8];
-    const int at = (int)((shift < 0 ? word << 2 : word >> shift) & 0x3cu);
-    const float level =
-        __builtin_rintf(__int_as_float(__builtin_amdgcn_ds_bpermute(at, __float_as_int(entry))) * rel[j / 16]);
-    float clamped = fminf(fmaxf(level, -127.0f), 127.0f);
-    if (KEEP_NAN && level != level) clamped = level;
-    v[j] = clamped * scale;
-  }
+  for (int j = 0; j < kLaneValues; ++j)
+    v[j] = fminf(fmaxf(__builtin_rintf(codebook_times(w, entry, rel, j)), -127.0f), 127.0f) * scale;
+}
+
+// Where codebook * relative is NaN the level is NaN, which the clamp above
+// dropped (Java's min and max keep it). That is where the entry is NaN, the
+// relative scale is NaN, or an infinite entry meets a zero scale (E4M3 has
+// no infinities): `bad[r]` has bit c set when code c is NaN with run r's
+// scale. A wave with any such bit puts the NaNs back.
+__device__ __forceinline__ void keep_nans(const uint32_t (&w)[8], const uint32_t (&bad)[4], float (&v)[kLaneValues]) {
+#pragma unroll
+  for (int j = 0; j < kLaneValues; ++j)
+    if ((bad[j / 16] >> (nibble_address(w, j) >> 2)) & 1u) v[j] = __builtin_nanf("");
 }
 
 // What decodes a rotated weight (ops/ConvRotParts.scala): scales F32, one a
@@ -188,19 +200,20 @@ __global__ void __launch_bounds__(kBlockWaves * kWave)
 #pragma unroll
     for (int r = 0; r < 4; ++r) rel_code[r] = parts.relative[rel_row + (first + 16 * r) / parts.group_size];
     float rel[4];
-    bool nan = !__builtin_isfinite(entry);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) rel[r] = e4m3(rel_code[r]);
+    // codes whose entry is NaN, or infinite (lanes 0-15 hold the 16 entries)
+    const uint32_t nan_codes = (uint32_t)__ballot(lane < 16 && entry != entry) & 0xffffu;
+    const uint32_t inf_codes = (uint32_t)__ballot(lane < 16 && __builtin_isinf(entry)) & 0xffffu;
+    uint32_t bad[4];
+    bool any = false;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      rel[r] = e4m3(rel_code[r]);
-      nan |= (rel_code[r] & 0x7fu) == 0x7fu;
+      bad[r] = rel[r] != rel[r] ? 0xffffu : nan_codes | (rel[r] == 0.0f ? inf_codes : 0u);
+      any |= bad[r] != 0;
     }
-    // codebook * relative is finite unless an entry or a relative scale is
-    // not, and then a wave takes the path that keeps NaNs
-    const bool clean = !__any(nan);
-    if (clean)
-      decode_nibbles<false>(w, entry, rel, scale, v);
-    else
-      decode_nibbles<true>(w, entry, rel, scale, v);
+    decode_nibbles(w, entry, rel, scale, v);
+    if (__any(any)) keep_nans(w, bad, v);
   }
 
   // digits 0, 1, 2 (strides 1, 4, 16) in registers
