@@ -290,6 +290,36 @@ __global__ void __launch_bounds__(256) decode_rows(const uint8_t* table, const i
   }
 }
 
+// Dense tables of any width and alignment (the reference's gather_rows_f32,
+// kernels/elementwise.hip:89-93, takes any width): a thread per value.
+__device__ __forceinline__ void store_value(float* p, float v) { *p = v; }
+__device__ __forceinline__ void store_value(uint16_t* p, float v) { *p = (uint16_t)bf16_bits(v); }
+__device__ __forceinline__ void store_value(Half* p, float v) { p->bits = __builtin_bit_cast(uint16_t, (_Float16)v); }
+
+template <typename T, int FORMAT>
+__global__ void __launch_bounds__(256) dense_values(const uint8_t* table, const int32_t* ids, T* out, int64_t count,
+                                                    int64_t vocab, int cols, int32_t* bad_id) {
+  const int64_t total = count * cols;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const int64_t t = i / cols;
+    const int64_t id = ids ? ids[t] : t;
+    float v = 0.0f;
+    if (id < 0 || id >= vocab) {
+      if (bad_id) *bad_id = 1;
+    } else {
+      const int64_t at = id * cols + (i - t * cols);
+      if constexpr (FORMAT == DRIFT_F32)
+        v = reinterpret_cast<const float*>(table)[at];
+      else if constexpr (FORMAT == DRIFT_F16)
+        v = f16_value(reinterpret_cast<const uint16_t*>(table)[at]);
+      else
+        v = __uint_as_float((uint32_t)reinterpret_cast<const uint16_t*>(table)[at] << 16);
+    }
+    store_value(out + i, v);
+  }
+}
+
 // ---------------------------------------------------------------- launch layer
 
 // A format's block and alignment, for the checks: values, bytes, alignment.
@@ -330,10 +360,30 @@ int decode_launch(const char* entry, const void* table, int32_t format, const in
   const Layout l = layout(format);
   if (l.values == 0) return refuse("%s: no storage type %d", entry, format);
   if (count < 0 || vocab < 0) return refuse("%s: %lld rows of %lld", entry, (long long)count, (long long)vocab);
-  if (cols <= 0 || cols % l.values != 0 || cols % 8 != 0)
+  const bool dense = l.values == 1;
+  if (cols <= 0 || cols % l.values != 0 || (!dense && cols % 8 != 0))
     return refuse("%s: rows of %d values are not whole blocks of %d (and chunks of 8)", entry, cols, l.values);
   if (count == 0) return 0;
   if (!table || !out) return refuse("%s: null table or out", entry);
+  const hipStream_t s = (hipStream_t)stream;
+  if (dense && (cols % 8 != 0 || !aligned16(out) || !aligned16(table))) {
+    // any width: element alignment only
+    if (reinterpret_cast<uintptr_t>(table) % (uintptr_t)l.bytes != 0 ||
+        reinterpret_cast<uintptr_t>(out) % sizeof(T) != 0)
+      return refuse("%s: the table or out is not aligned to its elements", entry);
+    const dim3 grid(grid_for(count * cols, 256, kOneShotBlocks));
+    const auto* bytes = static_cast<const uint8_t*>(table);
+    if (format == DRIFT_F32)
+      hipLaunchKernelGGL((dense_values<T, DRIFT_F32>), grid, dim3(256), 0, s, bytes, ids, out, count, vocab, cols,
+                         bad_id);
+    else if (format == DRIFT_F16)
+      hipLaunchKernelGGL((dense_values<T, DRIFT_F16>), grid, dim3(256), 0, s, bytes, ids, out, count, vocab, cols,
+                         bad_id);
+    else
+      hipLaunchKernelGGL((dense_values<T, DRIFT_BF16>), grid, dim3(256), 0, s, bytes, ids, out, count, vocab, cols,
+                         bad_id);
+    return launched(entry);
+  }
   if (!aligned16(out)) return refuse("%s: out is not 16-byte aligned", entry);
   if (reinterpret_cast<uintptr_t>(table) % (uintptr_t)l.align != 0)
     return refuse("%s: the table is not %d-byte aligned", entry, l.align);
@@ -341,7 +391,6 @@ int decode_launch(const char* entry, const void* table, int32_t format, const in
   const int64_t chunks = count * (cols / 8);
   const dim3 grid(grid_for(chunks, 256, kOneShotBlocks));
   const auto* bytes = static_cast<const uint8_t*>(table);
-  const hipStream_t s = (hipStream_t)stream;
   switch (format) {
 #define DRIFT_DECODE(CODE, F)                                                                                     \
   case CODE:                                                                                                     \

@@ -813,7 +813,8 @@ class HipOps:
             self._rotated(f"drift_rotated_embedding_{_suffix(out.dtype)}", table, out, ids, badId)
             return
         t = self._checkStored("embedding", table)
-        _require(table.cols % 8 == 0, f"embedding: rows of {table.cols} values (kernels take multiples of 8)")
+        _require(table.cols % 8 == 0 or t.values == 1,
+                 f"embedding: rows of {table.cols} values (quant kernels take multiples of 8)")
         _on_device("embedding", table.data, ids, out)
         vocab, cols = table.shape
         if t.name == "Q8_0":
@@ -859,7 +860,8 @@ class HipOps:
         t = self._checkStored("dequantize", table)
         _require(out.dtype in (BF16, F16), f"dequantize writes BF16 or F16, not {_name(out.dtype)}")
         _require(tuple(out.shape) == table.shape, f"dequantize: out {_shape(out)} for a table {list(table.shape)}")
-        _require(table.cols % 8 == 0, f"dequantize: rows of {table.cols} values (kernels take multiples of 8)")
+        _require(table.cols % 8 == 0 or t.values == 1,
+                 f"dequantize: rows of {table.cols} values (quant kernels take multiples of 8)")
         _on_device("dequantize", table.data, out)
         entry = "drift_dequantize_bf16" if out.dtype == BF16 else "drift_dequantize_f16"
         self._launch(entry, _ptr(table.data), t.ggmlId, _ptr(out), table.shape[0], table.cols)

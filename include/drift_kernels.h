@@ -346,12 +346,14 @@ int drift_embedding_q8_0_bf16(const uint8_t* table, const int32_t* ids, uint16_t
 
 /* Rows `ids` of a table of storage type `format` ([vocab, cols] values, each
  * row whole blocks: 32 values for the 32-value quants, 256 for the K-quants
- * and IQ4_XS, cols a multiple of 8), decoded as the type's decoder in the
- * reference does (bit-exact, BF16 the F32 value rounded to nearest even),
- * into out [count, cols]. The table must be aligned to its blocks' fields
- * (2 bytes for Q4_0, Q5_0, Q8_0, Q6_K, IQ4_NL, ROCmFP4; 4 for Q4_1, Q5_1; 8
- * for Q4_K, Q5_K, IQ4_XS; 1 for ROCmFP4 fast; 16 for F32, F16, BF16) and out
- * 16-byte aligned. Ids outside [0, vocab) as drift_embedding_q8_0 (which Q8_0
+ * and IQ4_XS, cols a multiple of 8; dense F32, F16, BF16 rows of any width),
+ * decoded as the type's decoder in the reference does (bit-exact, BF16 the
+ * F32 value rounded to nearest even), into out [count, cols]. The table must
+ * be aligned to its blocks' fields (2 bytes for Q4_0, Q5_0, Q8_0, Q6_K,
+ * IQ4_NL, ROCmFP4; 4 for Q4_1, Q5_1; 8 for Q4_K, Q5_K, IQ4_XS; 1 for ROCmFP4
+ * fast) and out 16-byte aligned; dense tables need only their elements
+ * aligned (16-byte aligned ones with rows of multiples of 8 take 16-byte
+ * loads). Ids outside [0, vocab) as drift_embedding_q8_0 (which Q8_0
  * tables take). Replaces kernels/matvec.hip:830-839 gather<T> and its
  * gather_<q> instances (:891-897, :942-954) and elementwise.hip:89-93
  * gather_rows_f32 (ops/HipLinear.scala:21-52; CPU ops/CpuLinear.scala:12-41). */

@@ -93,3 +93,29 @@ def test_misaligned_tables_are_refused(hip):
     step("embedding Q4_K from a table 4 bytes off an 8-byte boundary")
     with pytest.raises(_lib.HipError, match="8-byte aligned"):
         hip.embedding(shifted, dev_i32(np.zeros(1, np.int32)), out)
+
+
+@pytest.mark.parametrize("name", ["F32", "F16", "BF16"])
+@pytest.mark.parametrize("cols", [1, 3, 100])
+def test_dense_tables_of_any_width(hip, name, cols):
+    # gather_rows_f32 (kernels/elementwise.hip:89-93) takes any width; so do
+    # the dense types here, through their per-value path
+    vocab = 19
+    raw, table = table_of(name, vocab, cols, 31 + cols)
+    ids = np.random.default_rng(32).integers(-1, vocab + 1, 45).astype(np.int32)
+    step(f"embedding {name} rows of {cols}")
+    good = (ids >= 0) & (ids < vocab)
+    want = np.zeros((ids.size, cols), np.float32)
+    want[good] = o.embedding(name, raw, vocab, cols, ids[good])
+    out = torch.empty((ids.size, cols), dtype=torch.float32, device=DEV)
+    bad = torch.zeros(1, dtype=torch.int32, device=DEV)
+    hip.embedding(table, dev_i32(ids), out, bad)
+    assert_bits(want.view(np.uint32), host_f32(out).view(np.uint32), what=f"{name} width {cols}")
+    assert int(bad.item()) == int((~good).any())
+    bf = torch.empty((ids.size, cols), dtype=torch.bfloat16, device=DEV)
+    hip.embedding(table, dev_i32(ids), bf)
+    assert_bits(o.to_bf16(want), host_bits(bf), what=f"{name} width {cols} bf16")
+    dense = torch.empty((vocab, cols), dtype=torch.float16, device=DEV)
+    hip.dequantize(table, dense)
+    full = o.embedding(name, raw, vocab, cols, np.arange(vocab, dtype=np.int32))
+    assert_bits(full.astype(np.float16).view(np.uint16), host_bits(dense), what=f"{name} width {cols} f16")
