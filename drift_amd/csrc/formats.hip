@@ -46,9 +46,14 @@ __device__ __forceinline__ uint32_t byte_of(uint2 w, int k) { return ((k < 4 ? w
 __device__ __forceinline__ int nibble_of(uint2 w, int k, int shift) { return (int)((byte_of(w, k) >> shift) & 0xfu); }
 
 // IQuants.Values (tensor/IQuants.scala:14-16) and RocmFp4.Codebook
-// (tensor/RocmFp4.scala:21-22).
-__constant__ float kIq4Values[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
-__constant__ float kRocmCodebook[16] = {0, 1, 2, 3, 4, 6, 8, 10, 0, -1, -2, -3, -4, -6, -8, -10};
+// (tensor/RocmFp4.scala:21-22). A kernel copies its format's table into LDS
+// (`lut`) once: read per value with a lane's own index, a table in global
+// memory costs a vector load per value.
+__device__ __forceinline__ float lut_entry(int id, int i) {
+  constexpr float kIq4Values[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+  constexpr float kRocmCodebook[16] = {0, 1, 2, 3, 4, 6, 8, 10, 0, -1, -2, -3, -4, -6, -8, -10};
+  return id == 1 ? kIq4Values[i] : kRocmCodebook[i];
+}
 
 // RocmFp4.halfScale (tensor/RocmFp4.scala:27-39): half an unsigned E4M3 byte,
 // 0 past 0x7e.
@@ -64,7 +69,8 @@ __device__ __forceinline__ float rocm_half_scale(uint32_t byte) {
 
 struct Q4_0 {  // GgmlQuants.scala:13-29: d * (q - 8)
   static constexpr int kValues = 32, kBytes = 18, kAlign = 2;
-  __device__ static void decode(const uint8_t* b, int c, float (&v)[8]) {
+  static constexpr int kLut = 0;
+  __device__ static void decode(const uint8_t* b, int c, float (&v)[8], const float* lut) {
     const float d = f16_value(ld16(b));
     const uint2 w = bytes8<kAlign>(b + 2 + 8 * (c & 1));
 #pragma unroll
@@ -74,7 +80,8 @@ struct Q4_0 {  // GgmlQuants.scala:13-29: d * (q - 8)
 
 struct Q4_1 {  // :31-49: d * q + m
   static constexpr int kValues = 32, kBytes = 20, kAlign = 4;
-  __device__ static void decode(const uint8_t* b, int c, float (&v)[8]) {
+  static constexpr int kLut = 0;
+  __device__ static void decode(const uint8_t* b, int c, float (&v)[8], const float* lut) {
     const uint32_t dm = ld32(b);
     const float d = f16_value(dm & 0xffffu), m = f16_value(dm >> 16);
     const uint2 w = bytes8<kAlign>(b + 4 + 8 * (c & 1));
@@ -87,7 +94,8 @@ struct Q4_1 {  // :31-49: d * q + m
 template <bool MIN>
 struct Q5 {  // Q5_0 (:66-81) d * (q - 16); Q5_1 (:83-99) d * q + m
   static constexpr int kValues = 32, kBytes = MIN ? 24 : 22, kAlign = MIN ? 4 : 2;
-  __device__ static void decode(const uint8_t* b, int c, float (&v)[8]) {
+  static constexpr int kLut = 0;
+  __device__ static void decode(const uint8_t* b, int c, float (&v)[8], const float* lut) {
     float d, m = 0.0f;
     uint32_t qh;
     if constexpr (MIN) {
@@ -114,7 +122,8 @@ struct Q5 {  // Q5_0 (:66-81) d * (q - 16); Q5_1 (:83-99) d * q + m
 
 struct Q8_0 {  // :101-117: q * d (plain IEEE products; the Q8_0 gather kernel also matches x86's NaNs)
   static constexpr int kValues = 32, kBytes = 34, kAlign = 2;
-  __device__ static void decode(const uint8_t* b, int c, float (&v)[8]) {
+  static constexpr int kLut = 0;
+  __device__ static void decode(const uint8_t* b, int c, float (&v)[8], const float* lut) {
     const float d = f16_value(ld16(b));
     const uint2 w = bytes8<kAlign>(b + 2 + 8 * c);
 #pragma unroll
@@ -138,7 +147,8 @@ __device__ __forceinline__ void scale_and_min(const uint32_t (&s)[3], int j, int
 template <bool FIVE>
 struct QK45 {  // Q4_K (KQuants.scala:102-110), Q5_K (:112-121): d * sc * q - dmin * m, per 32
   static constexpr int kValues = 256, kBytes = FIVE ? 176 : 144, kAlign = 8;
-  __device__ static void decode(const uint8_t* b, int c, float (&v)[8]) {
+  static constexpr int kLut = 0;
+  __device__ static void decode(const uint8_t* b, int c, float (&v)[8], const float* lut) {
     const uint32_t dd = ld32(b);
     const uint32_t s[3] = {ld32(b + 4), ld32(b + 8), ld32(b + 12)};
     const int j = c / 4;  // the 32-value sub-block
@@ -162,7 +172,8 @@ struct QK45 {  // Q4_K (KQuants.scala:102-110), Q5_K (:112-121): d * sc * q - dm
 
 struct Q6_K {  // KQuants.scala:123-134: d * sc * (q - 32), q of six bits
   static constexpr int kValues = 256, kBytes = 210, kAlign = 2;
-  __device__ static void decode(const uint8_t* b, int c, float (&v)[8]) {
+  static constexpr int kLut = 0;
+  __device__ static void decode(const uint8_t* b, int c, float (&v)[8], const float* lut) {
     const int half = c / 16, r = c % 16;  // values 128 half + 8 r ..
     const uint2 low = bytes8<kAlign>(b + half * 64 + 8 * (r % 8));  // nibble 4 (r / 8) of ql[half 64 + r' % 64]
     const uint2 high = bytes8<kAlign>(b + 128 + half * 32 + 8 * (r % 4));  // KQuants.twoBits (:38-45)
@@ -177,17 +188,19 @@ struct Q6_K {  // KQuants.scala:123-134: d * sc * (q - 32), q of six bits
 
 struct IQ4_NL {  // IQuants.scala:18-47: d * Values(q)
   static constexpr int kValues = 32, kBytes = 18, kAlign = 2;
-  __device__ static void decode(const uint8_t* b, int c, float (&v)[8]) {
+  static constexpr int kLut = 1;
+  __device__ static void decode(const uint8_t* b, int c, float (&v)[8], const float* lut) {
     const float d = f16_value(ld16(b));
     const uint2 w = bytes8<kAlign>(b + 2 + 8 * (c & 1));
 #pragma unroll
-    for (int k = 0; k < 8; ++k) v[k] = d * kIq4Values[nibble_of(w, k, 4 * (c >> 1))];
+    for (int k = 0; k < 8; ++k) v[k] = d * lut[nibble_of(w, k, 4 * (c >> 1))];
   }
 };
 
 struct IQ4_XS {  // IQuants.scala:49-80: run i scaled by d * (ls - 32)
   static constexpr int kValues = 256, kBytes = 136, kAlign = 8;
-  __device__ static void decode(const uint8_t* b, int c, float (&v)[8]) {
+  static constexpr int kLut = 1;
+  __device__ static void decode(const uint8_t* b, int c, float (&v)[8], const float* lut) {
     const int i = c / 4, r = c % 4;  // run i, chunk r of its 4
     const float d = f16_value(ld16(b));
     const uint32_t high = ld16(b + 2);
@@ -196,18 +209,19 @@ struct IQ4_XS {  // IQuants.scala:49-80: run i scaled by d * (ls - 32)
     const float scale = d * (float)(ls - 32);
     const uint2 w = bytes8<kAlign>(b + 8 + 16 * i + 8 * (r & 1));
 #pragma unroll
-    for (int k = 0; k < 8; ++k) v[k] = scale * kIq4Values[nibble_of(w, k, 4 * (r >> 1))];
+    for (int k = 0; k < 8; ++k) v[k] = scale * lut[nibble_of(w, k, 4 * (r >> 1))];
   }
 };
 
 template <bool FAST>
 struct RocmFp4 {  // RocmFp4.scala:45-62: Codebook(q) * halfScale, a scale per half (one for FAST)
   static constexpr int kValues = 32, kBytes = FAST ? 17 : 18, kAlign = FAST ? 1 : 2;
-  __device__ static void decode(const uint8_t* b, int c, float (&v)[8]) {
+  static constexpr int kLut = 2;
+  __device__ static void decode(const uint8_t* b, int c, float (&v)[8], const float* lut) {
     const uint2 w = bytes8<kAlign>(b + 8 * (c & 1));
     const float scale = rocm_half_scale(ld8(b + (FAST ? 16 : 16 + (c >> 1))));
 #pragma unroll
-    for (int k = 0; k < 8; ++k) v[k] = kRocmCodebook[nibble_of(w, k, 4 * (c >> 1))] * scale;
+    for (int k = 0; k < 8; ++k) v[k] = lut[nibble_of(w, k, 4 * (c >> 1))] * scale;
   }
 };
 
@@ -215,7 +229,8 @@ struct RocmFp4 {  // RocmFp4.scala:45-62: Codebook(q) * halfScale, a scale per h
 template <int FORMAT>
 struct Dense {
   static constexpr int kValues = 1, kBytes = FORMAT == DRIFT_F32 ? 4 : 2, kAlign = 16;
-  __device__ static void decode(const uint8_t* b, int c, float (&v)[8]) {
+  static constexpr int kLut = 0;
+  __device__ static void decode(const uint8_t* b, int c, float (&v)[8], const float* lut) {
     if constexpr (FORMAT == DRIFT_F32) {
       float4 a = *reinterpret_cast<const float4*>(b + 32 * c), z = *reinterpret_cast<const float4*>(b + 32 * c + 16);
       v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = z.x, v[5] = z.y, v[6] = z.z, v[7] = z.w;
@@ -269,6 +284,11 @@ template <typename T, typename F>
 __global__ void __launch_bounds__(256) decode_rows(const uint8_t* table, const int32_t* ids, T* out, int64_t count,
                                                    int64_t vocab, int cols, int64_t row_bytes, int32_t* bad_id) {
   constexpr int kChunks = F::kValues / 8 > 0 ? F::kValues / 8 : 1;  // chunks per block
+  __shared__ float lut[16];
+  if constexpr (F::kLut != 0) {
+    if (threadIdx.x < 16) lut[threadIdx.x] = lut_entry(F::kLut, (int)threadIdx.x);
+    __syncthreads();
+  }
   const int per_row = cols / 8;
   const int64_t total = count * per_row;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
@@ -282,9 +302,9 @@ __global__ void __launch_bounds__(256) decode_rows(const uint8_t* table, const i
       for (int k = 0; k < 8; ++k) v[k] = 0.0f;
       if (bad_id) *bad_id = 1;
     } else if constexpr (F::kValues == 1) {
-      F::decode(table + id * row_bytes, q, v);
+      F::decode(table + id * row_bytes, q, v, lut);
     } else {
-      F::decode(table + id * row_bytes + (int64_t)(q / kChunks) * F::kBytes, q % kChunks, v);
+      F::decode(table + id * row_bytes + (int64_t)(q / kChunks) * F::kBytes, q % kChunks, v, lut);
     }
     store_chunk<T>(out + t * cols + (int64_t)q * 8, v);
   }
