@@ -133,6 +133,14 @@ __device__ __forceinline__ double group_sum(double v) {
   return v;
 }
 
+// Orders a wave's LDS writes before its lanes' reads of them, and back (the
+// lanes of one wave exchanging through LDS need no block barrier).
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // ---------------------------------------------------------------- int8 side output
 
 // Where a kernel also writes its output quantized for the runner's int8

@@ -92,13 +92,6 @@ __device__ __forceinline__ void load_codes(const uint8_t* p, uint32_t (&w)[Bytes
   }
 }
 
-// Orders a wave's LDS writes before its lanes' reads of them, and back.
-__device__ __forceinline__ void wave_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
 // 16 consecutive outputs as out holds them, into LDS: BF16 (32 bytes), or
 // F32 holding the BF16 value (ops/CpuLinear.scala:24-29; 64 bytes).
 __device__ __forceinline__ void stage_run(uint8_t* p, const float* v, uint16_t) {

@@ -70,9 +70,10 @@ __device__ __forceinline__ float rocm_half_scale(uint32_t byte) {
 struct Q4_0 {  // GgmlQuants.scala:13-29: d * (q - 8)
   static constexpr int kValues = 32, kBytes = 18, kAlign = 2;
   static constexpr int kLut = 0;
+  template <int A = kAlign>
   __device__ static void decode(const uint8_t* b, int c, float (&v)[8], const float* lut) {
     const float d = f16_value(ld16(b));
-    const uint2 w = bytes8<kAlign>(b + 2 + 8 * (c & 1));
+    const uint2 w = bytes8<A>(b + 2 + 8 * (c & 1));
 #pragma unroll
     for (int k = 0; k < 8; ++k) v[k] = d * (float)(nibble_of(w, k, 4 * (c >> 1)) - 8);
   }
@@ -81,10 +82,11 @@ struct Q4_0 {  // GgmlQuants.scala:13-29: d * (q - 8)
 struct Q4_1 {  // :31-49: d * q + m
   static constexpr int kValues = 32, kBytes = 20, kAlign = 4;
   static constexpr int kLut = 0;
+  template <int A = kAlign>
   __device__ static void decode(const uint8_t* b, int c, float (&v)[8], const float* lut) {
     const uint32_t dm = ld32(b);
     const float d = f16_value(dm & 0xffffu), m = f16_value(dm >> 16);
-    const uint2 w = bytes8<kAlign>(b + 4 + 8 * (c & 1));
+    const uint2 w = bytes8<A>(b + 4 + 8 * (c & 1));
 #pragma unroll
     for (int k = 0; k < 8; ++k) v[k] = d * (float)nibble_of(w, k, 4 * (c >> 1)) + m;
   }
@@ -95,6 +97,7 @@ template <bool MIN>
 struct Q5 {  // Q5_0 (:66-81) d * (q - 16); Q5_1 (:83-99) d * q + m
   static constexpr int kValues = 32, kBytes = MIN ? 24 : 22, kAlign = MIN ? 4 : 2;
   static constexpr int kLut = 0;
+  template <int A = kAlign>
   __device__ static void decode(const uint8_t* b, int c, float (&v)[8], const float* lut) {
     float d, m = 0.0f;
     uint32_t qh;
@@ -107,7 +110,7 @@ struct Q5 {  // Q5_0 (:66-81) d * (q - 16); Q5_1 (:83-99) d * q + m
       d = f16_value(ld16(b));
       qh = ld16(b + 2) | (ld16(b + 4) << 16);
     }
-    const uint2 w = bytes8<kAlign>(b + (MIN ? 8 : 6) + 8 * (c & 1));
+    const uint2 w = bytes8<A>(b + (MIN ? 8 : 6) + 8 * (c & 1));
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       const int j = 8 * c + k;
@@ -123,9 +126,10 @@ struct Q5 {  // Q5_0 (:66-81) d * (q - 16); Q5_1 (:83-99) d * q + m
 struct Q8_0 {  // :101-117: q * d (plain IEEE products; the Q8_0 gather kernel also matches x86's NaNs)
   static constexpr int kValues = 32, kBytes = 34, kAlign = 2;
   static constexpr int kLut = 0;
+  template <int A = kAlign>
   __device__ static void decode(const uint8_t* b, int c, float (&v)[8], const float* lut) {
     const float d = f16_value(ld16(b));
-    const uint2 w = bytes8<kAlign>(b + 2 + 8 * c);
+    const uint2 w = bytes8<A>(b + 2 + 8 * c);
 #pragma unroll
     for (int k = 0; k < 8; ++k) v[k] = (float)(int8_t)byte_of(w, k) * d;
   }
@@ -148,6 +152,7 @@ template <bool FIVE>
 struct QK45 {  // Q4_K (KQuants.scala:102-110), Q5_K (:112-121): d * sc * q - dmin * m, per 32
   static constexpr int kValues = 256, kBytes = FIVE ? 176 : 144, kAlign = 8;
   static constexpr int kLut = 0;
+  template <int A = kAlign>
   __device__ static void decode(const uint8_t* b, int c, float (&v)[8], const float* lut) {
     const uint32_t dd = ld32(b);
     const uint32_t s[3] = {ld32(b + 4), ld32(b + 8), ld32(b + 12)};
@@ -158,9 +163,9 @@ struct QK45 {  // Q4_K (KQuants.scala:102-110), Q5_K (:112-121): d * sc * q - dm
     const float m = f16_value(dd >> 16) * (float)min;
     // KQuants.nibble (:47-53): chunk j's values are the low (even j) or high
     // nibbles of the 32 bytes at (j / 2) * 32
-    const uint2 w = bytes8<kAlign>(b + (FIVE ? 48 : 16) + (j / 2) * 32 + 8 * (c % 4));
+    const uint2 w = bytes8<A>(b + (FIVE ? 48 : 16) + (j / 2) * 32 + 8 * (c % 4));
     uint2 h = make_uint2(0, 0);
-    if constexpr (FIVE) h = bytes8<kAlign>(b + 16 + 8 * (c % 4));  // the fifth bits, bit j of byte e % 32
+    if constexpr (FIVE) h = bytes8<A>(b + 16 + 8 * (c % 4));  // the fifth bits, bit j of byte e % 32
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       int q = nibble_of(w, k, 4 * (j % 2));
@@ -173,10 +178,11 @@ struct QK45 {  // Q4_K (KQuants.scala:102-110), Q5_K (:112-121): d * sc * q - dm
 struct Q6_K {  // KQuants.scala:123-134: d * sc * (q - 32), q of six bits
   static constexpr int kValues = 256, kBytes = 210, kAlign = 2;
   static constexpr int kLut = 0;
+  template <int A = kAlign>
   __device__ static void decode(const uint8_t* b, int c, float (&v)[8], const float* lut) {
     const int half = c / 16, r = c % 16;  // values 128 half + 8 r ..
-    const uint2 low = bytes8<kAlign>(b + half * 64 + 8 * (r % 8));  // nibble 4 (r / 8) of ql[half 64 + r' % 64]
-    const uint2 high = bytes8<kAlign>(b + 128 + half * 32 + 8 * (r % 4));  // KQuants.twoBits (:38-45)
+    const uint2 low = bytes8<A>(b + half * 64 + 8 * (r % 8));  // nibble 4 (r / 8) of ql[half 64 + r' % 64]
+    const uint2 high = bytes8<A>(b + 128 + half * 32 + 8 * (r % 4));  // KQuants.twoBits (:38-45)
     const float d = f16_value(ld16(b + 208)) * (float)(int8_t)ld8(b + 192 + c / 2);
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
@@ -189,9 +195,10 @@ struct Q6_K {  // KQuants.scala:123-134: d * sc * (q - 32), q of six bits
 struct IQ4_NL {  // IQuants.scala:18-47: d * Values(q)
   static constexpr int kValues = 32, kBytes = 18, kAlign = 2;
   static constexpr int kLut = 1;
+  template <int A = kAlign>
   __device__ static void decode(const uint8_t* b, int c, float (&v)[8], const float* lut) {
     const float d = f16_value(ld16(b));
-    const uint2 w = bytes8<kAlign>(b + 2 + 8 * (c & 1));
+    const uint2 w = bytes8<A>(b + 2 + 8 * (c & 1));
 #pragma unroll
     for (int k = 0; k < 8; ++k) v[k] = d * lut[nibble_of(w, k, 4 * (c >> 1))];
   }
@@ -200,6 +207,7 @@ struct IQ4_NL {  // IQuants.scala:18-47: d * Values(q)
 struct IQ4_XS {  // IQuants.scala:49-80: run i scaled by d * (ls - 32)
   static constexpr int kValues = 256, kBytes = 136, kAlign = 8;
   static constexpr int kLut = 1;
+  template <int A = kAlign>
   __device__ static void decode(const uint8_t* b, int c, float (&v)[8], const float* lut) {
     const int i = c / 4, r = c % 4;  // run i, chunk r of its 4
     const float d = f16_value(ld16(b));
@@ -207,7 +215,7 @@ struct IQ4_XS {  // IQuants.scala:49-80: run i scaled by d * (ls - 32)
     const uint32_t low = (ld8(b + 4 + i / 2) >> (4 * (i % 2))) & 0xfu;
     const int ls = (int)(low | (((high >> (2 * i)) & 3u) << 4));
     const float scale = d * (float)(ls - 32);
-    const uint2 w = bytes8<kAlign>(b + 8 + 16 * i + 8 * (r & 1));
+    const uint2 w = bytes8<A>(b + 8 + 16 * i + 8 * (r & 1));
 #pragma unroll
     for (int k = 0; k < 8; ++k) v[k] = scale * lut[nibble_of(w, k, 4 * (r >> 1))];
   }
@@ -217,8 +225,9 @@ template <bool FAST>
 struct RocmFp4 {  // RocmFp4.scala:45-62: Codebook(q) * halfScale, a scale per half (one for FAST)
   static constexpr int kValues = 32, kBytes = FAST ? 17 : 18, kAlign = FAST ? 1 : 2;
   static constexpr int kLut = 2;
+  template <int A = kAlign>
   __device__ static void decode(const uint8_t* b, int c, float (&v)[8], const float* lut) {
-    const uint2 w = bytes8<kAlign>(b + 8 * (c & 1));
+    const uint2 w = bytes8<A>(b + 8 * (c & 1));
     const float scale = rocm_half_scale(ld8(b + (FAST ? 16 : 16 + (c >> 1))));
 #pragma unroll
     for (int k = 0; k < 8; ++k) v[k] = lut[nibble_of(w, k, 4 * (c >> 1))] * scale;
@@ -230,6 +239,7 @@ template <int FORMAT>
 struct Dense {
   static constexpr int kValues = 1, kBytes = FORMAT == DRIFT_F32 ? 4 : 2, kAlign = 16;
   static constexpr int kLut = 0;
+  template <int A = kAlign>
   __device__ static void decode(const uint8_t* b, int c, float (&v)[8], const float* lut) {
     if constexpr (FORMAT == DRIFT_F32) {
       float4 a = *reinterpret_cast<const float4*>(b + 32 * c), z = *reinterpret_cast<const float4*>(b + 32 * c + 16);
@@ -340,6 +350,59 @@ __global__ void __launch_bounds__(256) dense_values(const uint8_t* table, const 
   }
 }
 
+// The 256-value formats (the K-quants, IQ4_XS) through LDS: each half wave
+// copies one block (144 to 210 bytes) into LDS with a few coalesced 4- or
+// 2-byte loads a lane, then its 32 lanes decode their chunks from there, so
+// the block's scales and fields are read from HBM once, not by every lane
+// with its own small loads. Two blocks a wave, waves independent.
+template <typename T, typename F>
+__global__ void __launch_bounds__(256) decode_staged(const uint8_t* table, const int32_t* ids, T* out, int64_t count,
+                                                     int64_t vocab, int cols, int64_t row_bytes, int32_t* bad_id) {
+  static_assert(F::kValues == 256, "a block is 32 chunks");
+  constexpr int kPad = (F::kBytes + 7) / 8 * 8;  // blocks on 8-byte boundaries: 8-byte field reads
+  constexpr int kPiece = F::kAlign >= 4 && F::kBytes % 4 == 0 ? 4 : 2;
+  constexpr int kPieces = F::kBytes / kPiece;
+  __shared__ __align__(16) uint8_t staged[8][kPad];
+  __shared__ float lut[16];
+  if constexpr (F::kLut != 0) {
+    if (threadIdx.x < 16) lut[threadIdx.x] = lut_entry(F::kLut, (int)threadIdx.x);
+    __syncthreads();
+  }
+  const int lane = (int)threadIdx.x & 63, wave = (int)threadIdx.x >> 6, half = lane >> 5, c = lane & 31;
+  uint8_t* mine = staged[wave * 2 + half];
+  const int per_row = cols / 256;
+  const int64_t blocks = count * per_row;
+  for (int64_t first = (int64_t)blockIdx.x * 8 + wave * 2; first < blocks; first += (int64_t)gridDim.x * 8) {
+    const int64_t block = min(first + half, blocks - 1);  // a half past the last block mirrors it
+    const int64_t t = block / per_row;
+    const int b = (int)(block - t * per_row);
+    const int64_t id = ids ? ids[t] : t;
+    const bool bad = id < 0 || id >= vocab;
+    const uint8_t* src = table + (bad ? 0 : id) * row_bytes + (int64_t)b * F::kBytes;
+#pragma unroll
+    for (int k = 0; k < (kPieces + 31) / 32; ++k) {
+      const int piece = c + 32 * k;
+      if (piece < kPieces) {
+        if constexpr (kPiece == 4)
+          *reinterpret_cast<uint32_t*>(mine + 4 * piece) = ld32(src + 4 * piece);
+        else
+          *reinterpret_cast<uint16_t*>(mine + 2 * piece) = (uint16_t)ld16(src + 2 * piece);
+      }
+    }
+    wave_sync();
+    float v[8];
+    if (bad) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) v[k] = 0.0f;
+      if (bad_id) *bad_id = 1;
+    } else {
+      F::template decode<8>(mine, c, v, lut);
+    }
+    if (first + half < blocks) store_chunk<T>(out + t * cols + (int64_t)b * 256 + c * 8, v);
+    wave_sync();  // the block's reads are done before the next copy
+  }
+}
+
 // ---------------------------------------------------------------- launch layer
 
 // A format's block and alignment, for the checks: values, bytes, alignment.
@@ -414,6 +477,14 @@ int decode_launch(const char* entry, const void* table, int32_t format, const in
   switch (format) {
 #define DRIFT_DECODE(CODE, F)                                                                                     \
   case CODE:                                                                                                     \
+    if constexpr (F::kValues == 256) {                                                                           \
+      if (vocab > 0) {                                                                                           \
+        const dim3 staged(grid_for(count * (cols / 256), 8, kOneShotBlocks));                                    \
+        hipLaunchKernelGGL((decode_staged<T, F>), staged, dim3(256), 0, s, bytes, ids, out, count, vocab, cols,    \
+                           row_bytes, bad_id);                                                                   \
+        break;                                                                                                   \
+      }                                                                                                          \
+    }                                                                                                            \
     hipLaunchKernelGGL((decode_rows<T, F>), grid, dim3(256), 0, s, bytes, ids, out, count, vocab, cols, row_bytes, \
                        bad_id);                                                                                  \
     break;
