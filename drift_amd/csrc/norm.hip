@@ -136,6 +136,41 @@ __global__ void __launch_bounds__(256) rms_norm_rows_scalar(T* x, const T* y, co
   }
 }
 
+// Narrow rows (at most 32 values, a pixel's channels, often millions of
+// rows): a thread per row, as the reference's rms_norm_narrow_f32
+// (kernels/norm.hip:414-426). The sum runs over the row in order, as the
+// CPU's left fold does, so the result is the CPU's to the last bit.
+constexpr int kNarrowCols = 32;
+
+template <typename T>
+__global__ void __launch_bounds__(256) rms_norm_narrow(T* x, const T* y, const float* weight, T* out, int64_t rows,
+                                                       int cols, float eps, float offset, int weight_rows) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t row = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; row < rows; row += stride) {
+    T* xr = x + row * cols;
+    const T* yr = y ? y + row * cols : nullptr;
+    float v[kNarrowCols];
+    double squares = 0.0;
+#pragma unroll
+    for (int c = 0; c < kNarrowCols; ++c) {
+      if (c < cols) {
+        v[c] = load_one(xr + c);
+        if (yr) v[c] += load_one(yr + c);
+        squares += (double)v[c] * (double)v[c];
+      }
+    }
+    const double factor = 1.0 / sqrt(squares / (double)cols + (double)eps);
+    const float* w = weight + (row % weight_rows) * cols;
+#pragma unroll
+    for (int c = 0; c < kNarrowCols; ++c) {
+      if (c < cols) {
+        if (yr) store_one(xr + c, v[c]);
+        store_one(out + row * cols + c, (float)((double)v[c] * factor * ((double)w[c] + (double)offset)));
+      }
+    }
+  }
+}
+
 // ------------------------------------------------------------------ LayerNorm / AdaLN
 
 // MODULATE false: out = normal * (weight or 1) + (bias or 0).
@@ -462,8 +497,12 @@ RowPlan plan_rows(int64_t rows, int cols, bool vector_ok) {
   RowPlan plan;
   if (!vector_ok || cols % N != 0) return plan;
   const int chunks = cols / N;
-  // few long rows: a 4-wave group per row shortens each lane's chain
-  plan.waves = (chunks > kWave * 16 || (rows < 1024 && chunks >= 4 * kWave)) ? 4 : 1;
+  // long rows: a 4-wave group per row shortens each lane's chain. The split
+  // depends on the row's width only, never on how many rows come with it, so
+  // a row's sum is taken in the same order (and is the same to the last bit)
+  // whether it is normed alone, as a decode step's token, or in a batch
+  plan.waves = chunks >= 4 * kWave ? 4 : 1;
+  (void)rows;
   const int per_lane = (int)ceil_div(chunks, kWave * plan.waves);
   static const int kSteps[] = {1, 2, 3, 4, 6, 8, 12, 16};
   for (int k : kSteps)
@@ -502,7 +541,10 @@ int rms_norm(const char* entry, T* x, const T* y, const float* weight, T* out, i
   // codes, else by a quantize_x launch over out right after
   const bool fused = q.xq && plan.per_lane > 0 && codes_storable(q.xq, Chunk<T>::N);
   const Quantized in_kernel = fused ? q : Quantized{nullptr, nullptr, nullptr};
-  if (plan.per_lane == 0) {
+  if (cols <= kNarrowCols && !q.xq) {
+    hipLaunchKernelGGL(rms_norm_narrow<T>, dim3(grid_for(rows, 256)), dim3(256), 0, s, x, y, weight, out, rows,
+                       (int)cols, eps, offset, (int)weight_rows);
+  } else if (plan.per_lane == 0) {
     hipLaunchKernelGGL(rms_norm_rows_scalar<T>, dim3(grid_for(rows, 1)), dim3(256), 0, s, x, y, weight, out, rows,
                        (int)cols, eps, offset, (int)weight_rows);
   } else {

@@ -68,6 +68,54 @@ def test_add_rms_norm(hip, dtype, shape):
         assert_bf16(want, host_bits(out), what="addRmsNorm bf16")
 
 
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("cols", [1, 3, 16, 32])
+def test_rms_norm_narrow_rows(hip, dtype, cols):
+    # rows of at most 32 values (a pixel's channels; the reference's
+    # rms_norm_narrow_f32): a thread per row, the row summed in order, so the
+    # result is the oracle's to the last bit; with a residual too
+    rows = 70001
+    step(f"rmsNorm {dtype} narrow [{rows}, {cols}]")
+    x, y = gaussian(21, (rows, cols), 3.0), gaussian(22, (rows, cols))
+    w = gaussian(23, cols)
+    if dtype == "f32":
+        out = torch.empty((rows, cols), dtype=torch.float32, device=DEV)
+        hip.rmsNorm(dev_f32(x), dev_f32(w), 1e-6, 0.5, out)
+        assert np.array_equal(host_f32(out), o.rms_norm(x, w, 1e-6, 0.5)), "narrow rmsNorm f32"
+        xd = dev_f32(x)
+        hip.addRmsNorm(xd, dev_f32(y), d.RowNorm(dev_f32(w), 1e-6, 0.0, out))
+        summed, want = o.rms_norm(x, w, 1e-6, 0.0, y=y)
+        assert np.array_equal(host_f32(xd), summed) and np.array_equal(host_f32(out), want), "narrow addRmsNorm"
+    else:
+        xb, yb = bf16_input(x), bf16_input(y)
+        out = torch.empty((rows, cols), dtype=torch.bfloat16, device=DEV)
+        hip.rmsNorm(dev_bf16(xb), dev_f32(w), 1e-6, 0.0, out)
+        assert np.array_equal(host_bits(out), o.rms_norm_bf16(xb, w, 1e-6)), "narrow rmsNorm bf16"
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("cols", [1024, 2048, 4096, 5120])
+def test_rms_norm_does_not_depend_on_the_batch(hip, dtype, cols):
+    # a row normed alone (a decode step's token) and inside a prefill batch
+    # gives the same bits (ops/HipNormalisation.scala:82-88 asks this of the
+    # reference's kernel)
+    rows = 2048
+    step(f"rmsNorm {dtype} [{rows}, {cols}] against its rows one at a time")
+    x = gaussian(31, (rows, cols), 2.0)
+    w = (1 + 0.1 * gaussian(32, cols)).astype(np.float32)
+    if dtype == "f32":
+        xs, tt, host = dev_f32(x), torch.float32, host_f32
+    else:
+        xs, tt, host = dev_bf16(bf16_input(x)), torch.bfloat16, host_bits
+    batch = torch.empty((rows, cols), dtype=tt, device=DEV)
+    hip.rmsNorm(xs, dev_f32(w), 1e-6, 0.0, batch)
+    for r in (0, 1, 777, rows - 1):
+        alone = torch.empty((1, cols), dtype=tt, device=DEV)
+        hip.rmsNorm(xs[r:r + 1], dev_f32(w), 1e-6, 0.0, alone)
+        got, want = host(alone)[0], host(batch)[r]
+        assert np.array_equal(got.view(np.uint8), want.view(np.uint8)), f"row {r}"
+
+
 def test_rms_norm_in_place_and_zero_rows(hip):
     step("rmsNorm in place, zero row")
     x = gaussian(8, (6, 512))
