@@ -78,7 +78,7 @@ SIGNATURES = {
     "drift_convert": (_I32, [_P, _P, _I64, _I32, _P]),
 }
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 
 class NotBuilt(RuntimeError):

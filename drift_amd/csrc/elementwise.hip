@@ -194,6 +194,21 @@ __global__ void __launch_bounds__(256) convert_kernel(const void* x, void* out, 
       case DRIFT_F32_TO_F16:
         static_cast<_Float16*>(out)[i] = (_Float16) static_cast<const float*>(x)[i];
         break;
+      case DRIFT_F8E4M3_TO_F32: {
+        // fp8 E4M3 "fn" (tensor/DType.scala:105-115): bias 7, no infinities,
+        // NaN at S.1111.111
+        const uint32_t code = static_cast<const uint8_t*>(x)[i];
+        const int exponent = (int)((code >> 3) & 0xfu), mantissa = (int)(code & 7u);
+        float magnitude;
+        if (exponent == 0xf && mantissa == 7)
+          magnitude = __builtin_nanf("");
+        else if (exponent == 0)
+          magnitude = ldexpf((float)mantissa, -9);
+        else
+          magnitude = ldexpf((float)(8 + mantissa), exponent - 10);
+        static_cast<float*>(out)[i] = (code & 0x80u) ? -magnitude : magnitude;
+        break;
+      }
       default:
         static_cast<float*>(out)[i] = (float)static_cast<const _Float16*>(x)[i];
         break;
@@ -309,7 +324,7 @@ extern "C" int drift_convert(const void* x, void* out, int64_t n, int32_t kind, 
   const char* entry = "drift_convert";
   clear_error();
   if (n < 0) return refuse("%s: %lld values", entry, (long long)n);
-  if (kind < DRIFT_F32_TO_BF16 || kind > DRIFT_F16_TO_F32) return refuse("%s: no conversion %d", entry, kind);
+  if (kind < DRIFT_F32_TO_F16 || kind > DRIFT_F8E4M3_TO_F32) return refuse("%s: no conversion %d", entry, kind);
   if (n == 0) return 0;
   if (!x || !out) return refuse("%s: null x or out", entry);
   if (x == out) return refuse("%s: x and out are the same buffer of different types", entry);

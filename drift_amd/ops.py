@@ -412,11 +412,14 @@ def checkSplitHalves(x, first, second) -> None:
              f"splitHalves: {_shape(x)} into {_shape(first)}")
 
 
-_CONVERSIONS = {(F32, BF16): 0, (BF16, F32): 1, (F32, F16): 2, (F16, F32): 3}
+# ops/HipBase.scala:268-274's codes (fp8 E4M3 bytes as uint8 or float8_e4m3fn)
+_CONVERSIONS = {(F32, F16): 0, (F32, BF16): 1, (F16, F32): 2, (BF16, F32): 3, (torch.uint8, F32): 4,
+                (torch.float8_e4m3fn, F32): 4}
 
 
 def checkConvert(x, out) -> int:
-    """ops/MemoryOps.scala:68-84, for the float types."""
+    """ops/MemoryOps.scala:68-84: F32 to F16 or BF16, those to F32, and fp8
+    E4M3 to F32."""
     requireSameShape("convert", x, out)
     kind = _CONVERSIONS.get((x.dtype, out.dtype))
     _require(kind is not None, f"convert: no conversion from {_name(x.dtype)} to {_name(out.dtype)}")

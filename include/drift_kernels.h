@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define DRIFT_ABI_VERSION 5
+#define DRIFT_ABI_VERSION 6
 
 /* Activation kinds: src/drift/runner/ops/Activation.scala:6-20. */
 enum {
@@ -78,13 +78,15 @@ enum {
   DRIFT_Q4_0_ROCMFP4_FAST = 101
 };
 
-/* Conversions: src/drift/runner/ops/HipBase.scala:268-274 (codes of
- * kernels/elementwise.hip:68-86), restricted to the float types. */
+/* Conversions: the reference's codes, src/drift/runner/ops/HipBase.scala:
+ * 268-274 (kernels/elementwise.hip:68-86), so a caller passes the kind it
+ * passed before. */
 enum {
-  DRIFT_F32_TO_BF16 = 0,
-  DRIFT_BF16_TO_F32 = 1,
-  DRIFT_F32_TO_F16 = 2,
-  DRIFT_F16_TO_F32 = 3
+  DRIFT_F32_TO_F16 = 0,
+  DRIFT_F32_TO_BF16 = 1,
+  DRIFT_F16_TO_F32 = 2,
+  DRIFT_BF16_TO_F32 = 3,
+  DRIFT_F8E4M3_TO_F32 = 4
 };
 
 /* The ABI version this library implements (DRIFT_ABI_VERSION). */
@@ -412,7 +414,9 @@ int drift_rotated_dequantize_bf16(const void* codes, const float* scales, int64_
                                   int32_t cols, void* stream);
 
 /* ---------------------------------------------------------------- convert
- * Elementwise type conversion of n values (kinds above). Replaces
+ * Elementwise type conversion of n values (kinds above: F32 to F16 and BF16
+ * to nearest even, F16 and BF16 to F32 exactly, fp8 E4M3 "fn" bytes to F32
+ * as tensor/DType.scala:105-115 decodes them). Replaces
  * kernels/elementwise.hip:68-86 convert (CPU ops/CpuMemory.scala:84-109). */
 int drift_convert(const void* x, void* out, int64_t n, int32_t kind, void* stream);
 

@@ -23,7 +23,7 @@ def test_header_and_library_agree(lib):
 
 
 def test_version_and_error_text(lib):
-    assert lib.drift_abi_version() == _lib.ABI_VERSION == 5
+    assert lib.drift_abi_version() == _lib.ABI_VERSION == 6
     assert lib.drift_error_string(0).decode().lower().startswith("no error")
     assert lib.drift_error_string(1)
 
@@ -55,6 +55,7 @@ def test_elementwise_refuses_bad_arguments(lib):
     assert "no activation 5" in refused(lib, "drift_activation_f32", p, p, 10, 5, 1.0, NULL)
     assert "no activation -1" in refused(lib, "drift_gated_bf16", p, p, p, 10, -1, NULL, NULL, NULL, NULL)
     assert "no conversion 7" in refused(lib, "drift_convert", p, ctypes.c_void_p(32), 10, 7, NULL)
+    assert "no conversion 5" in refused(lib, "drift_convert", p, ctypes.c_void_p(32), 10, 5, NULL)
     assert "same buffer" in refused(lib, "drift_convert", p, p, 10, 0, NULL)
     assert lib.drift_activation_bf16(NULL, NULL, 0, 1, 1.0, NULL) == 0
 

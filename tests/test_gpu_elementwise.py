@@ -136,3 +136,19 @@ def test_convert_round_trips(hip):
     bo = torch.empty(1003, dtype=torch.bfloat16, device=DEV)
     hip.convert(dev_f32(odd), bo)
     assert_bits(o.to_bf16(odd), host_bits(bo), what="odd length")
+
+
+def test_convert_fp8_e4m3_to_f32(hip):
+    # the reference's conversion code 4 (ops/HipBase.scala:268-274): every
+    # E4M3 "fn" byte, as uint8 or torch's float8_e4m3fn, against the
+    # oracle's DType.F8E4M3 decode (pinned to torch's float8_e4m3fn)
+    codes = np.tile(np.arange(256, dtype=np.uint8), 5)
+    want = np.array([o.f8e4m3(c) for c in codes], np.float32)
+    nan = np.isnan(want)
+    for source in (torch.from_numpy(codes).to(DEV), torch.from_numpy(codes).to(DEV).view(torch.float8_e4m3fn)):
+        step(f"convert {source.dtype} -> f32")
+        out = torch.empty(codes.size, dtype=torch.float32, device=DEV)
+        hip.convert(source, out)
+        got = host_f32(out)
+        assert np.array_equal(np.isnan(got), nan)
+        assert_bits(want[~nan].view(np.uint32), got[~nan].view(np.uint32), what="fp8 e4m3")
