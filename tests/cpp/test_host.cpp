@@ -1,0 +1,446 @@
+// Tests of the C++ host side (drift_amd/host): `--checks` runs on the CPU the
+// shape and dtype refusals with the reference's messages (object Ops's
+// `require`s, as the reference's CPU suite meets them) and a refusal of the
+// library surfacing as a HipException, launching nothing; `--gpu` runs
+// operations on the device through HipOps and holds them to the oracle
+// (oracle/cpu_ops.h, the reference's CPU arithmetic restated in C) at the
+// bars the Python parity tests use: F32 |a - e| <= 1e-6 + 1e-5 |e|, BF16
+// within 1 ulp, gathers and decodes bit-exact.
+#include <hip/hip_runtime_api.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <functional>
+#include <random>
+#include <string>
+#include <vector>
+
+#include "../../drift_amd/host/drift_ops.hpp"
+#include "../../oracle/cpu_ops.h"
+
+using namespace drift;
+
+namespace {
+
+int failures = 0;
+std::vector<std::pair<std::string, std::function<void()>>>& registry(bool gpu) {
+  static std::vector<std::pair<std::string, std::function<void()>>> cpu, device;
+  return gpu ? device : cpu;
+}
+
+struct Register {
+  Register(bool gpu, const char* name, std::function<void()> body) { registry(gpu).emplace_back(name, body); }
+};
+
+#define CHECK_TEST(name) \
+  static void name();    \
+  static Register reg_##name(false, #name, name);\
+  static void name()
+#define GPU_TEST(name) \
+  static void name();  \
+  static Register reg_##name(true, #name, name);\
+  static void name()
+
+struct Failure : std::runtime_error {
+  using std::runtime_error::runtime_error;
+};
+
+void expect(bool condition, const std::string& what) {
+  if (!condition) throw Failure(what);
+}
+
+// `body` must throw `E` whose message contains `needle`.
+template <typename E = std::invalid_argument>
+void refused(const std::function<void()>& body, const std::string& needle) {
+  try {
+    body();
+  } catch (const E& e) {
+    expect(std::string(e.what()).find(needle) != std::string::npos,
+           "message \"" + std::string(e.what()) + "\" lacks \"" + needle + "\"");
+    return;
+  }
+  throw Failure("not refused: expected \"" + needle + "\"");
+}
+
+// A tensor at a made-up device address: the checks never dereference it.
+Tensor fake(DType dtype, Shape shape, uintptr_t address = 4096) {
+  return Tensor{dtype, std::move(shape), reinterpret_cast<void*>(address)};
+}
+
+// ---------------------------------------------------------------- checks (CPU)
+
+CHECK_TEST(row_wise_checks_carry_the_reference_messages) {
+  HipOps hip;
+  const Tensor x = fake(DType::F32, {3, 7}), w = fake(DType::F32, {7});
+  refused([&] { hip.rmsNorm(x, w, 1e-6f, 0.0f, fake(DType::F32, {3, 8})); },
+          "requirement failed: rmsNorm needs equal shapes, got [3×7], [3×8]");
+  refused([&] { hip.rmsNorm(x, fake(DType::F32, {6}), 1e-6f, 0.0f, x); }, "rmsNorm: [6] for rows of 7");
+  refused([&] { hip.rmsNorm(fake(DType::I32, {3, 7}), w, 1e-6f, 0.0f, fake(DType::I32, {3, 7})); },
+          "rmsNorm takes F32 or BF16, not I32");
+  refused([&] { hip.rmsNorm(x, w, 1e-6f, 0.0f, fake(DType::BF16, {3, 7})); },
+          "rmsNorm takes one type, not F32 and BF16");
+  refused([&] { hip.rmsNorm(x, fake(DType::BF16, {7}), 1e-6f, 0.0f, x); }, "rmsNorm takes F32, not BF16");
+  refused([&] { hip.layerNorm(fake(DType::BF16, {3, 7}), nullptr, nullptr, 1e-6f, fake(DType::BF16, {3, 7})); },
+          "layerNorm takes F32, not BF16");
+  refused([&] { hip.addRmsNorm(x, fake(DType::F32, {3, 6}), RowNorm{w, 1e-6f, 0.0f, x}); },
+          "addRmsNorm needs equal shapes, got [3×7], [3×6]");
+}
+
+CHECK_TEST(modulation_and_gates_are_checked) {
+  HipOps hip;
+  const Tensor x = fake(DType::BF16, {4, 8}), table = fake(DType::F32, {4, 48});
+  refused([&] { hip.modulateChunks(x, table, 3, 6, x); },
+          "modulateChunks: table [4×48] for [4×8], chunks ArraySeq(3, 6)");
+  refused([&] { hip.gatedAddChunk(x, x, fake(DType::F32, {5, 48}), 1); },
+          "gatedAddChunk: table [5×48] for [4×8], chunks ArraySeq(1)");
+  refused([&] { hip.rowGatedAdd(x, x, fake(DType::F32, {3})); }, "rowGatedAdd: gate [3] for [4×8]");
+  refused([&] { hip.gatedAdd(x, x, fake(DType::F32, {2, 8}), 0); }, "gatedAdd: per-sample gates need rowsPerSample");
+  refused([&] { hip.gatedAdd(x, x, fake(DType::F32, {3, 8}), 2); }, "gatedAdd: [3×8] for 2 samples of rows of 8");
+  refused([&] { hip.layerNormModulate(x, fake(DType::F32, {2, 8}), fake(DType::F32, {2, 8}), 1e-6f, x, 1); },
+          "layerNormModulate: 2 samples of 1 rows for 4 rows");
+  refused([&] { hip.layerNormModulate(x, fake(DType::F32, {2, 7}), fake(DType::F32, {2, 7}), 1e-6f, x); },
+          "layerNormModulate: scale [2×7], shift [2×7] for rows of 8");
+}
+
+CHECK_TEST(rope_rules) {
+  HipOps hip;
+  const Tensor x = fake(DType::F32, {5, 2, 128});
+  const Rope neox{1e4f, 128, RopeLayout::Neox, RopeSections::Single()};
+  refused([&] { hip.rope(x, fake(DType::F32, {5}), neox, x); }, "rope positions are I32, not F32");
+  refused([&] { hip.rope(x, fake(DType::I32, {4}), neox, x); }, "rope positions [4], expected [5]");
+  refused([&] { hip.rope(x, fake(DType::I32, {5}), Rope{1e4f, 130, RopeLayout::Neox, {}}, x); },
+          "rope: 130 rotary dimensions in heads of 128");
+  const Rope axes{1e4f, 128, RopeLayout::Interleaved, RopeSections::Axes({16, 24, 23})};
+  refused([&] { hip.rope(x, fake(DType::I32, {3, 5}), axes, x); }, "rope: axes of [16, 24, 23] pairs for 128");
+  const Rope mrope{1e6f, 128, RopeLayout::Neox, RopeSections::Contiguous(16, 24, 24)};
+  refused([&] { hip.rope(x, fake(DType::I32, {5}), mrope, x); }, "rope positions [5], expected [3×5]");
+  refused([&] { hip.rope(fake(DType::F32, {5, 256}), fake(DType::I32, {5}), neox, fake(DType::F32, {5, 256})); },
+          "rope takes [tokens, heads, headDimension], got [5×256]");
+  refused([&] { hip.ropeTable(x, fake(DType::F32, {5, 65}), fake(DType::F32, {5, 65}), x); },
+          "ropeTable: tables [5×65], [5×65] for [5×2×128]");
+  QueryKeyNorms norms{fake(DType::F32, {128}), fake(DType::F32, {64}), 1e-6f, 0.0f, neox};
+  refused([&] {
+    hip.queryKeyNormRope(x, fake(DType::F32, {5, 1, 128}), norms, fake(DType::I32, {5}), x,
+                         fake(DType::F32, {5, 1, 128}));
+  }, "queryKeyNormRope: keyNorm [64] for heads of 128");
+}
+
+CHECK_TEST(cache_and_attention_inputs_are_checked) {
+  HipOps hip;
+  refused([&] { KvCache::of(fake(DType::F16, {2, 8, 2, 64}), fake(DType::F16, {2, 2, 64, 8}), 8); },
+          "pages of 8 tokens: not a multiple of 16");
+  refused([&] { KvCache::of(fake(DType::F16, {2, 16, 2, 64}), fake(DType::F16, {2, 2, 16, 64}), 16); },
+          "cache values [2×2×16×64] for keys [2×16×2×64]");
+  const KvCache cache = KvCache::of(fake(DType::F16, {2, 16, 2, 64}), fake(DType::F16, {2, 2, 64, 16}), 16);
+  const Tensor k = fake(DType::BF16, {20, 2, 64});
+  refused([&] { hip.cacheWrite(k, k, cache, fake(DType::I32, {1}), 0); }, "a page table of 1 pages for 20 positions");
+  refused([&] { hip.cacheWrite(fake(DType::BF16, {20, 3, 64}), fake(DType::BF16, {20, 3, 64}), cache,
+                               fake(DType::I32, {2}), 0); },
+          "cacheWrite: [20×3×64] into a cache of 2 heads of 64");
+  refused([&] { hip.cacheWrite(k, k, cache, fake(DType::F32, {2}), 0); }, "a page table is I32 [pages], not F32 [2]");
+  refused([&] { hip.splitHalves(fake(DType::F32, {4, 10}), fake(DType::F32, {4, 4}), fake(DType::F32, {4, 4})); },
+          "splitHalves: [4×10] into [4×4]");
+  const Rope rope{1e6f, 64, RopeLayout::Neox, {}};
+  QueryKeyNorms norms{fake(DType::F32, {64}), fake(DType::F32, {64}), 1e-6f, 0.0f, rope};
+  refused([&] {
+    hip.queryKeyNormRopeCache(fake(DType::BF16, {20, 4, 1024}), k, k, norms, fake(DType::I32, {20}), cache,
+                              fake(DType::I32, {2}), 0, fake(DType::BF16, {20, 4, 1024}));
+  }, "queryKeyNormRopeCache: queries [20×4×1024]");
+}
+
+CHECK_TEST(tables_are_checked) {
+  HipOps hip;
+  const StorageType& q4k = StorageType::named("Q4_K");
+  const StoredTable table{fake(DType::U8, {10, 144}), &q4k, 256};
+  refused([&] { hip.embedding(table, fake(DType::I8, {3}), fake(DType::F32, {3, 256})); },
+          "embedding ids are I32 [tokens], not I8 [3]");
+  refused([&] { hip.embedding(table, fake(DType::I32, {3}), fake(DType::F32, {4, 256})); },
+          "embedding: out [4×256] for 3 rows of 256");
+  refused([&] { hip.embedding(StoredTable{fake(DType::U8, {10, 140}), &q4k, 256}, fake(DType::I32, {3}),
+                              fake(DType::F32, {3, 256})); },
+          "embedding: Q4_K bytes [10×140] for rows of 256");
+  refused([&] { hip.dequantize(table, fake(DType::F32, {10, 256})); }, "dequantize writes BF16 or F16, not F32");
+  refused([&] { hip.rotated(fake(DType::U8, {4, 256}), ConvRotParts{fake(DType::F32, {4}), {}}); },
+          "rotated: U8 codes [4×256]");
+  refused([&] { hip.rotated(fake(DType::I8, {4, 200}), ConvRotParts{fake(DType::F32, {4}), {}}); },
+          "rotated: rows of 200 columns");
+  refused([&] { hip.rotated(fake(DType::I8, {4, 256}), ConvRotParts{fake(DType::F32, {3}), {}}); },
+          "rotated: 3 F32 scales for 4 rows");
+  const ConvRotLevels levels{fake(DType::F32, {16}), fake(DType::U8, {4, 16}), 24};
+  refused([&] { hip.rotated(fake(DType::I8, {4, 256}), ConvRotParts{fake(DType::F32, {4}), levels}); },
+          "rotated: 512 columns in groups of 24");
+  const RotatedTable rotated = hip.rotated(fake(DType::I8, {4, 256}), ConvRotParts{fake(DType::F32, {1}), {}});
+  expect(rotated.shape() == Shape({4, 256}) && std::string(rotated.dtype()) == "CONVROT_I8", "rotated shape");
+  refused([&] { hip.convert(rotated, fake(DType::F32, {4, 256})); }, "convert: no conversion from CONVROT_I8 to F32");
+  refused([&] { hip.convert(fake(DType::BF16, {4}), fake(DType::F16, {4})); },
+          "convert: no conversion from BF16 to F16");
+}
+
+CHECK_TEST(library_refusals_are_hip_exceptions) {
+  // shapes the checks accept, a table 4 bytes off the 8-byte alignment Q4_K's
+  // fields need: the library refuses before launching anything
+  HipOps hip;
+  const StorageType& q4k = StorageType::named("Q4_K");
+  const StoredTable shifted{fake(DType::U8, {3, 144}, 4100), &q4k, 256};
+  refused<HipException>([&] { hip.embedding(shifted, fake(DType::I32, {1}), fake(DType::F32, {1, 256})); },
+                        "8-byte aligned");
+  try {
+    hip.embedding(shifted, fake(DType::I32, {1}), fake(DType::F32, {1, 256}));
+  } catch (const HipException& e) {
+    expect(e.entry == "drift_embedding_f32" && e.code == 1, "the exception names the entry point and code");
+  }
+}
+
+// ---------------------------------------------------------------- GPU parity
+
+void hip_check(hipError_t status, const char* what) {
+  if (status != hipSuccess) throw Failure(std::string(what) + ": " + hipGetErrorString(status));
+}
+
+// Device memory for a test, freed at scope end.
+struct Device {
+  std::vector<void*> owned;
+  ~Device() {
+    for (void* p : owned) (void)hipFree(p);
+  }
+  template <typename T>
+  Tensor upload(DType dtype, Shape shape, const std::vector<T>& host) {
+    void* p = nullptr;
+    const size_t bytes = host.size() * sizeof(T);
+    hip_check(hipMalloc(&p, bytes ? bytes : 16), "hipMalloc");
+    owned.push_back(p);
+    if (bytes) hip_check(hipMemcpy(p, host.data(), bytes, hipMemcpyHostToDevice), "hipMemcpy");
+    return Tensor{dtype, std::move(shape), p};
+  }
+  Tensor empty(DType dtype, Shape shape) {
+    void* p = nullptr;
+    const int64_t bytes = Tensor{dtype, shape, nullptr}.byteSize();
+    hip_check(hipMalloc(&p, (size_t)(bytes ? bytes : 16)), "hipMalloc");
+    owned.push_back(p);
+    return Tensor{dtype, std::move(shape), p};
+  }
+  template <typename T>
+  std::vector<T> download(const Tensor& t) {
+    std::vector<T> host((size_t)(t.byteSize() / (int64_t)sizeof(T)));
+    hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize");
+    hip_check(hipMemcpy(host.data(), t.data, host.size() * sizeof(T), hipMemcpyDeviceToHost), "hipMemcpy");
+    return host;
+  }
+};
+
+std::vector<float> gaussian(uint64_t seed, size_t n, float scale = 1.0f) {
+  std::mt19937_64 rng(seed);
+  std::normal_distribution<float> normal(0.0f, scale);
+  std::vector<float> v(n);
+  for (float& x : v) x = normal(rng);
+  return v;
+}
+
+std::vector<uint16_t> to_bf16(const std::vector<float>& x) {
+  std::vector<uint16_t> b(x.size());
+  oracle_f32_to_bf16_n(x.data(), b.data(), (int64_t)x.size());
+  return b;
+}
+
+std::vector<float> from_bf16(const std::vector<uint16_t>& b) {
+  std::vector<float> x(b.size());
+  oracle_bf16_to_f32_n(b.data(), x.data(), (int64_t)b.size());
+  return x;
+}
+
+void close_f32(const std::vector<float>& want, const std::vector<float>& got, const char* what) {
+  expect(want.size() == got.size(), std::string(what) + ": sizes");
+  for (size_t i = 0; i < want.size(); ++i) {
+    const bool both_nan = std::isnan(want[i]) && std::isnan(got[i]);
+    const bool ok = both_nan || std::fabs((double)got[i] - want[i]) <= 1e-6 + 1e-5 * std::fabs((double)want[i]);
+    if (!ok) throw Failure(std::string(what) + ": index " + std::to_string(i) + " got " + std::to_string(got[i]) +
+                           " want " + std::to_string(want[i]));
+  }
+}
+
+int64_t ordered(uint16_t b) { return (b & 0x8000) ? -(int64_t)(b & 0x7fff) : (int64_t)b; }
+
+void within_ulp(const std::vector<uint16_t>& want, const std::vector<uint16_t>& got, const char* what) {
+  expect(want.size() == got.size(), std::string(what) + ": sizes");
+  for (size_t i = 0; i < want.size(); ++i)
+    if (std::llabs(ordered(want[i]) - ordered(got[i])) > 1)
+      throw Failure(std::string(what) + ": index " + std::to_string(i) + " beyond 1 ulp");
+}
+
+template <typename T>
+void exact(const std::vector<T>& want, const std::vector<T>& got, const char* what) {
+  expect(want.size() == got.size() && std::memcmp(want.data(), got.data(), want.size() * sizeof(T)) == 0,
+         std::string(what) + ": not bit-exact");
+}
+
+GPU_TEST(rms_norm_f32_and_bf16) {
+  HipOps hip;
+  Device dev;
+  const int64_t rows = 5, cols = 4097;
+  std::vector<float> x = gaussian(1, rows * cols, 3.0f), w = gaussian(2, cols);
+  const Tensor xd = dev.upload(DType::F32, {rows, cols}, x), wd = dev.upload(DType::F32, {cols}, w);
+  const Tensor out = dev.empty(DType::F32, {rows, cols});
+  hip.rmsNorm(xd, wd, 1e-6f, 1.0f, out);
+  std::vector<float> want(x.size());
+  oracle_rms_norm(x.data(), nullptr, w.data(), want.data(), rows, cols, 1e-6f, 1.0f, 1);
+  close_f32(want, dev.download<float>(out), "rmsNorm f32");
+
+  const int64_t r2 = 8, c2 = 4096;
+  std::vector<uint16_t> xb = to_bf16(gaussian(3, r2 * c2));
+  std::vector<float> w2 = gaussian(4, c2);
+  const Tensor xbd = dev.upload(DType::BF16, {r2, c2}, xb), w2d = dev.upload(DType::F32, {c2}, w2);
+  const Tensor outb = dev.empty(DType::BF16, {r2, c2});
+  hip.rmsNorm(xbd, w2d, 1e-5f, 0.0f, outb);
+  std::vector<float> xf = from_bf16(xb), wantf(xf.size());
+  oracle_rms_norm(xf.data(), nullptr, w2.data(), wantf.data(), r2, c2, 1e-5f, 0.0f, 1);
+  within_ulp(to_bf16(wantf), dev.download<uint16_t>(outb), "rmsNorm bf16");
+}
+
+GPU_TEST(adaln_bf16_two_samples) {
+  HipOps hip;
+  Device dev;
+  const int64_t rows = 64, cols = 3072, per = 32;
+  std::vector<uint16_t> xb = to_bf16(gaussian(5, rows * cols));
+  std::vector<float> scale = gaussian(6, 2 * cols, 0.1f), shift = gaussian(7, 2 * cols, 0.1f);
+  const Tensor x = dev.upload(DType::BF16, {rows, cols}, xb);
+  const Tensor sc = dev.upload(DType::F32, {2, cols}, scale), sh = dev.upload(DType::F32, {2, cols}, shift);
+  const Tensor out = dev.empty(DType::BF16, {rows, cols});
+  hip.layerNormModulate(x, sc, sh, 1e-6f, out, per);
+  std::vector<float> xf = from_bf16(xb), normed(xf.size()), want(xf.size());
+  oracle_layer_norm(xf.data(), nullptr, nullptr, normed.data(), rows, cols, 1e-6f);
+  for (int s = 0; s < 2; ++s)
+    oracle_modulate(normed.data() + s * per * cols, scale.data() + s * cols, shift.data() + s * cols,
+                    want.data() + s * per * cols, per, cols);
+  within_ulp(to_bf16(want), dev.download<uint16_t>(out), "layerNormModulate bf16");
+}
+
+GPU_TEST(activations_and_gated) {
+  HipOps hip;
+  Device dev;
+  const int64_t n = 100003;
+  std::vector<float> g = gaussian(8, n, 3.0f), u = gaussian(9, n);
+  std::vector<uint16_t> gb = to_bf16(g);
+  const Tensor gbd = dev.upload(DType::BF16, {n}, gb), outb = dev.empty(DType::BF16, {n});
+  hip.activation(Activation::GeluTanh, gbd, outb);
+  std::vector<float> gf = from_bf16(gb), want(n);
+  oracle_activation(1, 1.0f, gf.data(), want.data(), n);
+  within_ulp(to_bf16(want), dev.download<uint16_t>(outb), "GELU-tanh bf16");
+  const Tensor gd = dev.upload(DType::F32, {n}, g), ud = dev.upload(DType::F32, {n}, u);
+  const Tensor out = dev.empty(DType::F32, {n});
+  hip.gated(Activation::Silu, gd, ud, out);
+  std::vector<float> want2(n);
+  oracle_gated(0, g.data(), u.data(), want2.data(), n);
+  close_f32(want2, dev.download<float>(out), "SwiGLU f32");
+}
+
+GPU_TEST(gated_residuals_per_sample) {
+  HipOps hip;
+  Device dev;
+  const int64_t rows = 48, cols = 3072, per = 24;
+  std::vector<float> x = gaussian(10, rows * cols), y = gaussian(11, rows * cols), gate = gaussian(12, 2 * cols);
+  const Tensor xd = dev.upload(DType::F32, {rows, cols}, x), yd = dev.upload(DType::F32, {rows, cols}, y);
+  hip.gatedAdd(xd, yd, dev.upload(DType::F32, {2, cols}, gate), per);
+  oracle_gated_add(x.data(), y.data(), gate.data(), rows, cols, per);
+  close_f32(x, dev.download<float>(xd), "gatedAdd per sample");
+}
+
+GPU_TEST(rope_neox_f32) {
+  HipOps hip;
+  Device dev;
+  const int tokens = 37, heads = 3, dim = 128;
+  std::vector<float> x = gaussian(13, (size_t)tokens * heads * dim);
+  std::vector<int32_t> positions(tokens);
+  for (int t = 0; t < tokens; ++t) positions[t] = (t * 131) % 4096;
+  const Tensor xd = dev.upload(DType::F32, {tokens, heads, dim}, x);
+  const Tensor pd = dev.upload(DType::I32, {tokens}, positions), out = dev.empty(DType::F32, {tokens, heads, dim});
+  hip.rope(xd, pd, Rope{1e6f, dim, RopeLayout::Neox, {}}, out);
+  std::vector<float> want(x.size());
+  const int32_t s[4] = {0, 0, 0, 0};
+  oracle_rope(x.data(), positions.data(), want.data(), tokens, heads, dim, dim, 1e6f, 0, 0, s);
+  close_f32(want, dev.download<float>(out), "rope NeoX f32");
+}
+
+GPU_TEST(q8_0_embedding_bit_exact) {
+  HipOps hip;
+  Device dev;
+  const int64_t vocab = 300, cols = 512, count = 77, row_bytes = cols / 32 * 34;
+  std::mt19937_64 rng(14);
+  std::vector<uint8_t> table((size_t)(vocab * row_bytes));
+  for (size_t i = 0; i < table.size(); ++i) table[i] = (uint8_t)rng();
+  for (int64_t b = 0; b < vocab * cols / 32; ++b) {  // finite fp16 scales
+    const uint16_t d = oracle_f32_to_f16(std::ldexp(1.0f + (float)(rng() % 1000) / 1000.0f, -8));
+    std::memcpy(&table[(size_t)(b * 34)], &d, 2);
+  }
+  std::vector<int32_t> ids(count);
+  for (auto& id : ids) id = (int32_t)(rng() % vocab);
+  const StoredTable t{dev.upload(DType::U8, {vocab, row_bytes}, table), &StorageType::named("Q8_0"), cols};
+  const Tensor out = dev.empty(DType::BF16, {count, cols});
+  hip.embedding(t, dev.upload(DType::I32, {count}, ids), out);
+  std::vector<float> want((size_t)(count * cols));
+  expect(oracle_embedding_q8_0(table.data(), vocab, cols, ids.data(), count, want.data()) == -1, "ids in range");
+  exact(to_bf16(want), dev.download<uint16_t>(out), "Q8_0 embedding bf16");
+}
+
+GPU_TEST(convrot_four_bit_decode_bit_exact) {
+  HipOps hip;
+  Device dev;
+  const int64_t rows = 9, cols = 768, group = 32;
+  std::mt19937_64 rng(15);
+  std::vector<uint8_t> codes((size_t)(rows * cols / 2)), relative((size_t)(rows * cols / group));
+  for (auto& c : codes) c = (uint8_t)rng();
+  for (auto& r : relative) r = (uint8_t)(0x58 + rng() % 0x1f);
+  std::vector<float> codebook = gaussian(16, 16, 0.5f), scales(rows);
+  for (auto& s : scales) s = 1e-4f + 1e-3f * (float)(rng() % 1000) / 1000.0f;
+  const ConvRotLevels levels{dev.upload(DType::F32, {16}, codebook),
+                             dev.upload(DType::U8, {rows, cols / group}, relative), (int)group};
+  const RotatedTable w = hip.rotated(dev.upload(DType::I8, {rows, cols / 2}, codes),
+                                     ConvRotParts{dev.upload(DType::F32, {rows}, scales), levels});
+  const Tensor out = dev.empty(DType::BF16, {rows, cols});
+  hip.convert(w, out);
+  std::vector<float> want((size_t)(rows * cols));
+  oracle_convrot_rows(codes.data(), scales.data(), rows, codebook.data(), relative.data(), group, cols, 0, rows,
+                      want.data());
+  exact(to_bf16(want), dev.download<uint16_t>(out), "ConvRot 4-bit decode");
+}
+
+GPU_TEST(fp8_convert_bit_exact) {
+  HipOps hip;
+  Device dev;
+  std::vector<uint8_t> codes(256);
+  for (int i = 0; i < 256; ++i) codes[i] = (uint8_t)i;
+  const Tensor out = dev.empty(DType::F32, {256});
+  hip.convert(dev.upload(DType::F8E4M3, {256}, codes), out);
+  std::vector<float> got = dev.download<float>(out);
+  for (int i = 0; i < 256; ++i) {
+    const float want = oracle_f8e4m3(i);
+    expect((std::isnan(want) && std::isnan(got[i])) || std::memcmp(&want, &got[i], 4) == 0,
+           "fp8 code " + std::to_string(i));
+  }
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+  const bool gpu = argc > 1 && std::string(argv[1]) == "--gpu";
+  if (argc < 2 || (!gpu && std::string(argv[1]) != "--checks")) {
+    std::printf("usage: test_host --checks | --gpu\n");
+    return 2;
+  }
+  int count = 0;
+  for (auto& [name, body] : registry(gpu)) {
+    ++count;
+    std::printf("[%s] %s ... ", gpu ? "gpu" : "cpu", name.c_str());
+    std::fflush(stdout);
+    try {
+      body();
+      std::printf("ok\n");
+    } catch (const std::exception& e) {
+      ++failures;
+      std::printf("FAILED: %s\n", e.what());
+    }
+    std::fflush(stdout);
+  }
+  std::printf("%d tests, %d failed\n", count, failures);
+  return failures ? 1 : 0;
+}
