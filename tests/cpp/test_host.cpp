@@ -18,6 +18,7 @@
 
 #include "../../drift_amd/host/drift_ops.hpp"
 #include "../../oracle/cpu_ops.h"
+#include "comparison.hpp"
 
 using namespace drift;
 
@@ -192,6 +193,21 @@ CHECK_TEST(library_refusals_are_hip_exceptions) {
   }
 }
 
+CHECK_TEST(comparison_rule_as_the_reference_states_it) {
+  using testing::Comparison;
+  using testing::Tolerance;
+  const float nan = std::nanf(""), inf = INFINITY;
+  expect(Comparison::of({1.0f, nan, inf, -inf}, {1.0f, nan, inf, -inf}, Tolerance{}).passed(),
+         "equal values, NaN with NaN, infinities with themselves");
+  const Comparison c = Comparison::of({1.0f, nan, inf, 0.0f, 2.0f}, {1.5f, 0.0f, -inf, nan, 2.0f}, Tolerance{0.25, 0.0});
+  expect(c.mismatches == 4 && c.firstMismatch == 0 && c.maxAbsolute == 0.5 && c.maxRelative == 0.5,
+         "mismatches " + c.summary());
+  expect(Comparison::of({100.0f}, {100.9f}, Tolerance{0.0, 1e-2}).passed() &&
+             !Comparison::of({100.0f}, {101.1f}, Tolerance{0.0, 1e-2}).passed(),
+         "relative part scales with |expected|");
+  refused([] { Comparison::of({1.0f}, {1.0f, 2.0f}, Tolerance{}); }, "comparing 2 values with 1");
+}
+
 // ---------------------------------------------------------------- GPU parity
 
 void hip_check(hipError_t status, const char* what) {
@@ -249,14 +265,10 @@ std::vector<float> from_bf16(const std::vector<uint16_t>& b) {
   return x;
 }
 
+// F32 results: the reference's rule at the F32 bar.
 void close_f32(const std::vector<float>& want, const std::vector<float>& got, const char* what) {
-  expect(want.size() == got.size(), std::string(what) + ": sizes");
-  for (size_t i = 0; i < want.size(); ++i) {
-    const bool both_nan = std::isnan(want[i]) && std::isnan(got[i]);
-    const bool ok = both_nan || std::fabs((double)got[i] - want[i]) <= 1e-6 + 1e-5 * std::fabs((double)want[i]);
-    if (!ok) throw Failure(std::string(what) + ": index " + std::to_string(i) + " got " + std::to_string(got[i]) +
-                           " want " + std::to_string(want[i]));
-  }
+  const testing::Comparison c = testing::Comparison::of(want, got, testing::Tolerance{1e-6, 1e-5});
+  if (!c.passed()) throw Failure(std::string(what) + ": " + c.summary());
 }
 
 int64_t ordered(uint16_t b) { return (b & 0x8000) ? -(int64_t)(b & 0x7fff) : (int64_t)b; }
@@ -417,6 +429,45 @@ GPU_TEST(fp8_convert_bit_exact) {
     expect((std::isnan(want) && std::isnan(got[i])) || std::memcmp(&want, &got[i], 4) == 0,
            "fp8 code " + std::to_string(i));
   }
+}
+
+// Callers write over an input (out aliases x): per-head rmsNorm in place
+// (models/DenseDecoder.scala:834-851), modulate(normed, ..., normed)
+// (models/Wan.scala:432), activation(up, up) (:474) and gated(gate, up,
+// gate) (models/DenseDecoder.scala:927).
+GPU_TEST(outputs_may_alias_their_inputs) {
+  HipOps hip;
+  Device dev;
+  const int64_t rows = 4096 * 8 / 64, cols = 128;
+  std::vector<float> x = gaussian(17, rows * cols), w = gaussian(18, cols);
+  const Tensor xd = dev.upload(DType::F32, {rows, cols}, x), wd = dev.upload(DType::F32, {cols}, w);
+  hip.rmsNorm(xd, wd, 1e-6f, 0.0f, xd);
+  std::vector<float> want(x.size());
+  oracle_rms_norm(x.data(), nullptr, w.data(), want.data(), rows, cols, 1e-6f, 0.0f, 1);
+  close_f32(want, dev.download<float>(xd), "rmsNorm in place");
+
+  const int64_t r2 = 6, c2 = 3072;
+  std::vector<float> n = gaussian(19, r2 * c2), scale = gaussian(20, c2, 0.1f), shift = gaussian(21, c2, 0.1f);
+  const Tensor nd = dev.upload(DType::F32, {r2, c2}, n);
+  hip.modulate(nd, dev.upload(DType::F32, {c2}, scale), dev.upload(DType::F32, {c2}, shift), nd);
+  std::vector<float> want2(n.size());
+  oracle_modulate(n.data(), scale.data(), shift.data(), want2.data(), r2, c2);
+  close_f32(want2, dev.download<float>(nd), "modulate in place");
+
+  const int64_t count = 3 * 14336;
+  std::vector<uint16_t> up = to_bf16(gaussian(22, count, 2.0f));
+  const Tensor upd = dev.upload(DType::BF16, {count}, up);
+  hip.activation(Activation::GeluTanh, upd, upd);
+  std::vector<float> upf = from_bf16(up), want3(count);
+  oracle_activation(1, 1.0f, upf.data(), want3.data(), count);
+  within_ulp(to_bf16(want3), dev.download<uint16_t>(upd), "activation in place");
+
+  std::vector<float> g = gaussian(23, count), u = gaussian(24, count);
+  const Tensor gd = dev.upload(DType::F32, {count}, g);
+  hip.gated(Activation::Silu, gd, dev.upload(DType::F32, {count}, u), gd);
+  std::vector<float> want4(count);
+  oracle_gated(0, g.data(), u.data(), want4.data(), count);
+  close_f32(want4, dev.download<float>(gd), "gated into its gate");
 }
 
 }  // namespace

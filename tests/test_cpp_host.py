@@ -14,7 +14,7 @@ PROGRAM = os.path.join(ROOT, "tests", "cpp", "test_host")
 
 
 def _sources():
-    return [os.path.join(ROOT, "tests", "cpp", "test_host.cpp"),
+    return [os.path.join(ROOT, "tests", "cpp", "test_host.cpp"), os.path.join(ROOT, "tests", "cpp", "comparison.hpp"),
             os.path.join(ROOT, "drift_amd", "host", "drift_ops.cpp"),
             os.path.join(ROOT, "drift_amd", "host", "drift_ops.hpp")]
 
