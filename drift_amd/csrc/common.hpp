@@ -133,6 +133,36 @@ __device__ __forceinline__ double group_sum(double v) {
   return v;
 }
 
+// The same butterfly for a 32-bit value and an exact, order-free combine
+// (max of floats, sum of integers): every lane of an aligned group of `width`
+// lanes gets the group's result.
+template <int kCtrl>
+__device__ __forceinline__ int dpp_move32(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, kCtrl, 0xf, 0xf, true);
+}
+
+template <int width>
+__device__ __forceinline__ float group_max(float v) {
+  if constexpr (width > 1) v = fmaxf(v, __int_as_float(dpp_move32<0xb1>(__float_as_int(v))));
+  if constexpr (width > 2) v = fmaxf(v, __int_as_float(dpp_move32<0x4e>(__float_as_int(v))));
+  if constexpr (width > 4) v = fmaxf(v, __int_as_float(dpp_move32<0x141>(__float_as_int(v))));
+  if constexpr (width > 8) v = fmaxf(v, __int_as_float(dpp_move32<0x140>(__float_as_int(v))));
+#pragma unroll
+  for (int mask = 16; mask < width; mask <<= 1) v = fmaxf(v, __shfl_xor(v, mask, width));
+  return v;
+}
+
+template <int width>
+__device__ __forceinline__ int group_sum_int(int v) {
+  if constexpr (width > 1) v += dpp_move32<0xb1>(v);
+  if constexpr (width > 2) v += dpp_move32<0x4e>(v);
+  if constexpr (width > 4) v += dpp_move32<0x141>(v);
+  if constexpr (width > 8) v += dpp_move32<0x140>(v);
+#pragma unroll
+  for (int mask = 16; mask < width; mask <<= 1) v += __shfl_xor(v, mask, width);
+  return v;
+}
+
 // Orders a wave's LDS writes before its lanes' reads of them, and back (the
 // lanes of one wave exchanging through LDS need no block barrier).
 __device__ __forceinline__ void wave_sync() {
@@ -177,8 +207,7 @@ __device__ __forceinline__ void quantize_chunk(const float (&v)[N], int64_t bloc
   float amax = fabsf(v[0]);
 #pragma unroll
   for (int j = 1; j < N; ++j) amax = fmaxf(amax, fabsf(v[j]));
-#pragma unroll
-  for (int mask = 1; mask < G; mask <<= 1) amax = fmaxf(amax, __shfl_xor(amax, mask, G));
+  amax = group_max<G>(amax);
   const float d = amax / 127.0f;
   int sum = 0;
   uint32_t bytes[(N + 3) / 4] = {};
@@ -197,8 +226,7 @@ __device__ __forceinline__ void quantize_chunk(const float (&v)[N], int64_t bloc
     *reinterpret_cast<uint32_t*>(at) = bytes[0];
   else
     *reinterpret_cast<uint2*>(at) = make_uint2(bytes[0], bytes[1]);
-#pragma unroll
-  for (int mask = 1; mask < G; mask <<= 1) sum += __shfl_xor(sum, mask, G);
+  sum = group_sum_int<G>(sum);
   if (member == 0) {
     q.xd[block] = d;
     q.xs[block] = d * (float)sum;

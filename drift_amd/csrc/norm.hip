@@ -53,6 +53,19 @@ __device__ __forceinline__ void load_f32(const float* p, float (&v)[N]) {
 
 // ------------------------------------------------------------------ RMSNorm
 
+// A chunk's squares, summed in order in double. A row's sum of squares is
+// taken as: per lane, its chunks' sums in increasing chunk order, then over
+// the wave, then over the row's waves in order; with four waves a row, wave s
+// holding the lane's chunks 64 * (4m + s) + lane. rms_norm_rows and
+// rms_norm_wide keep that order, so a row norms the same in either.
+template <int N>
+__device__ __forceinline__ double chunk_squares(const float (&v)[N]) {
+  double p = 0.0;
+#pragma unroll
+  for (int j = 0; j < N; ++j) p += (double)v[j] * (double)v[j];
+  return p;
+}
+
 // With q.xq, out is quantized too as it is written (quantize_chunk; cols a
 // multiple of 32, so a row holds whole blocks).
 template <typename T, int K, int W>
@@ -68,6 +81,18 @@ __global__ void __launch_bounds__(256) rms_norm_rows(T* x, const T* y, const flo
   for (int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + wave / W; row < rows;
        row += (int64_t)gridDim.x * kRowsPerBlock) {
     T* xr = x + row * cols;
+    const float* w = weight + (row % weight_rows) * cols;
+    // Short rows (decode) are latency-bound: their weights are loaded with x,
+    // before the sum, so the two loads' latencies overlap.
+    constexpr bool kEarlyWeights = K * N <= 16;
+    float early[kEarlyWeights ? K : 1][N];
+    if constexpr (kEarlyWeights) {
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        const int c = (k * W + sub) * kWave + lane;
+        if (c < chunks) load_f32<N>(w + c * N, early[k]);
+      }
+    }
     float v[K][N];
     double squares = 0.0;
 #pragma unroll
@@ -81,20 +106,23 @@ __global__ void __launch_bounds__(256) rms_norm_rows(T* x, const T* y, const flo
 #pragma unroll
           for (int j = 0; j < N; ++j) v[k][j] += u[j];  // the F32 sum, as add() rounds it
         }
-#pragma unroll
-        for (int j = 0; j < N; ++j) squares += (double)v[k][j] * (double)v[k][j];
+        squares += chunk_squares(v[k]);
       }
     }
     squares = row_sum<W>(squares, partial);
     const double factor = 1.0 / sqrt(squares / (double)cols + (double)eps);
-    const float* w = weight + (row % weight_rows) * cols;
 #pragma unroll
     for (int k = 0; k < K; ++k) {
       const int c = (k * W + sub) * kWave + lane;
       if (c < chunks) {
         if (y) Chunk<T>::store(xr + c * N, v[k]);  // the residual stream, before out (which may be x)
         float wv[N], o[N];
-        load_f32<N>(w + c * N, wv);
+        if constexpr (kEarlyWeights) {
+#pragma unroll
+          for (int j = 0; j < N; ++j) wv[j] = early[k][j];
+        } else {
+          load_f32<N>(w + c * N, wv);
+        }
 #pragma unroll
         for (int j = 0; j < N; ++j) o[j] = (float)((double)v[k][j] * factor * ((double)wv[j] + (double)offset));
         Chunk<T>::store(out + row * cols + c * N, o);
@@ -104,6 +132,79 @@ __global__ void __launch_bounds__(256) rms_norm_rows(T* x, const T* y, const flo
         }
       }
     }
+  }
+}
+
+// Few rows (a decode step's tokens): a row's chunks spread over W = 8 or 16
+// waves (512 or 1024 threads), so each lane's serial work is 2 or 4 times
+// shorter than in the four-wave group. The chunks' sums of squares go through
+// LDS to the first four waves, which add them in the four-wave group's order
+// (chunk_squares), so the result is the same to the last bit.
+template <typename T, int K, int W>
+__global__ void __launch_bounds__(64 * W) rms_norm_wide(T* x, const T* y, const float* weight, T* out, int64_t rows,
+                                                       int cols, float eps, float offset, int weight_rows,
+                                                       Quantized q) {
+  static_assert(W == 8 || W == 16, "the wide group is 8 or 16 waves");
+  constexpr int N = Chunk<T>::N;
+  constexpr int kSlots = K * W;  // 64-chunk slots a row can have
+  __shared__ double sums[kSlots][kWave];
+  __shared__ double partial[4];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int chunks = cols / N;
+  for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
+    T* xr = x + row * cols;
+    const float* w = weight + (row % weight_rows) * cols;
+    float wv[K][N];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const int c = (k * W + wave) * kWave + lane;
+      if (c < chunks) load_f32<N>(w + c * N, wv[k]);
+    }
+    float v[K][N];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const int slot = k * W + wave, c = slot * kWave + lane;
+      if (c < chunks) {
+        Chunk<T>::load(xr + c * N, v[k]);
+        if (y) {
+          float u[N];
+          Chunk<T>::load(y + row * cols + c * N, u);
+#pragma unroll
+          for (int j = 0; j < N; ++j) v[k][j] += u[j];
+        }
+        sums[slot][lane] = chunk_squares(v[k]);
+      }
+    }
+    __syncthreads();
+    if (wave < 4) {
+      double squares = 0.0;
+#pragma unroll
+      for (int m = 0; m < kSlots / 4; ++m) {
+        const int slot = 4 * m + wave;
+        if (slot * kWave + lane < chunks) squares += sums[slot][lane];
+      }
+      squares = group_sum<64>(squares);
+      if (lane == 0) partial[wave] = squares;
+    }
+    __syncthreads();
+    const double total = ((partial[0] + partial[1]) + partial[2]) + partial[3];
+    const double factor = 1.0 / sqrt(total / (double)cols + (double)eps);
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const int c = (k * W + wave) * kWave + lane;
+      if (c < chunks) {
+        if (y) Chunk<T>::store(xr + c * N, v[k]);
+        float o[N];
+#pragma unroll
+        for (int j = 0; j < N; ++j) o[j] = (float)((double)v[k][j] * factor * ((double)wv[k][j] + (double)offset));
+        Chunk<T>::store(out + row * cols + c * N, o);
+        if (q.xq) {
+          as_written<T>(o);
+          quantize_chunk<N>(o, (row * cols + c * N) / 32, q);
+        }
+      }
+    }
+    __syncthreads();  // sums and partial are reused by the next row
   }
 }
 
@@ -523,6 +624,20 @@ RowPlan plan_rows(int64_t rows, int cols, bool vector_ok) {
   MACRO(12)                    \
   MACRO(16)
 
+// Rows for rms_norm_wide: a few (at most one a CU) long rows, spread over 8
+// waves (one or two chunks a lane) or 16 (one to four). 0: the four-wave
+// group (or one wave) of plan_rows.
+constexpr int64_t kWideRows = 256;
+
+template <typename T>
+int wide_waves(int64_t rows, int cols, const RowPlan& plan) {
+  const int chunks = cols / Chunk<T>::N;
+  if (plan.waves != 4 || rows > kWideRows || rows < 1) return 0;
+  if (chunks >= 16 * kWave && chunks <= 4 * 16 * kWave) return 16;
+  if (chunks >= 8 * kWave && chunks < 16 * kWave) return 8;
+  return 0;
+}
+
 template <typename T>
 int rms_norm(const char* entry, T* x, const T* y, const float* weight, T* out, int64_t rows, int32_t cols, float eps,
              float offset, int32_t weight_rows, Quantized q, void* stream) {
@@ -547,6 +662,27 @@ int rms_norm(const char* entry, T* x, const T* y, const float* weight, T* out, i
   } else if (plan.per_lane == 0) {
     hipLaunchKernelGGL(rms_norm_rows_scalar<T>, dim3(grid_for(rows, 1)), dim3(256), 0, s, x, y, weight, out, rows,
                        (int)cols, eps, offset, (int)weight_rows);
+  } else if (const int wide = wide_waves<T>(rows, cols, plan)) {
+    const int per_lane = (int)ceil_div(cols / Chunk<T>::N, kWave * wide);
+    const dim3 grid((unsigned)rows), block(kWave * wide);
+    if (wide == 8 && per_lane == 1)
+      hipLaunchKernelGGL((rms_norm_wide<T, 1, 8>), grid, block, 0, s, x, y, weight, out, rows, cols, eps, offset,
+                         weight_rows, in_kernel);
+    else if (wide == 8)
+      hipLaunchKernelGGL((rms_norm_wide<T, 2, 8>), grid, block, 0, s, x, y, weight, out, rows, cols, eps, offset,
+                         weight_rows, in_kernel);
+    else if (per_lane == 1)
+      hipLaunchKernelGGL((rms_norm_wide<T, 1, 16>), grid, block, 0, s, x, y, weight, out, rows, cols, eps, offset,
+                         weight_rows, in_kernel);
+    else if (per_lane == 2)
+      hipLaunchKernelGGL((rms_norm_wide<T, 2, 16>), grid, block, 0, s, x, y, weight, out, rows, cols, eps, offset,
+                         weight_rows, in_kernel);
+    else if (per_lane == 3)
+      hipLaunchKernelGGL((rms_norm_wide<T, 3, 16>), grid, block, 0, s, x, y, weight, out, rows, cols, eps, offset,
+                         weight_rows, in_kernel);
+    else
+      hipLaunchKernelGGL((rms_norm_wide<T, 4, 16>), grid, block, 0, s, x, y, weight, out, rows, cols, eps, offset,
+                         weight_rows, in_kernel);
   } else {
     const unsigned grid = grid_for(rows, 4 / plan.waves);
 #define DRIFT_RMS_CASE(K)                                                                                     \

@@ -46,7 +46,7 @@ def test_rms_norm_bf16(hip, shape):
 
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
-@pytest.mark.parametrize("shape", [(3, 7), (4, 4096), (600, 1024)])
+@pytest.mark.parametrize("shape", [(3, 7), (4, 4096), (3, 6144), (2, 16384), (600, 1024)])
 def test_add_rms_norm(hip, dtype, shape):
     step(f"addRmsNorm {dtype} {shape}")
     x, y = gaussian(5, shape), gaussian(6, shape)
@@ -94,11 +94,12 @@ def test_rms_norm_narrow_rows(hip, dtype, cols):
 
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
-@pytest.mark.parametrize("cols", [1024, 2048, 4096, 5120])
+@pytest.mark.parametrize("cols", [1024, 2048, 4096, 5120, 12288, 16384, 32768])
 def test_rms_norm_does_not_depend_on_the_batch(hip, dtype, cols):
     # a row normed alone (a decode step's token) and inside a prefill batch
     # gives the same bits (ops/HipNormalisation.scala:82-88 asks this of the
-    # reference's kernel)
+    # reference's kernel); a few rows take the 8- and 16-wave groups, a batch
+    # the 4-wave group
     rows = 2048
     step(f"rmsNorm {dtype} [{rows}, {cols}] against its rows one at a time")
     x = gaussian(31, (rows, cols), 2.0)
@@ -114,6 +115,9 @@ def test_rms_norm_does_not_depend_on_the_batch(hip, dtype, cols):
         hip.rmsNorm(xs[r:r + 1], dev_f32(w), 1e-6, 0.0, alone)
         got, want = host(alone)[0], host(batch)[r]
         assert np.array_equal(got.view(np.uint8), want.view(np.uint8)), f"row {r}"
+    few = torch.empty((7, cols), dtype=tt, device=DEV)
+    hip.rmsNorm(xs[100:107], dev_f32(w), 1e-6, 0.0, few)
+    assert np.array_equal(host(few).view(np.uint8), host(batch)[100:107].view(np.uint8)), "rows 100-106"
 
 
 def test_rms_norm_in_place_and_zero_rows(hip):
