@@ -181,6 +181,18 @@ def test_attention_inputs_qwen3_shape(hip, dtype, t, gated):
     run_attention_inputs(hip, dtype, t, 32, 8, 128, QWEN3_ROPE, start, table, pages, gated, 90 + t)
 
 
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("heads,kv,dim,gated", [(8, 3, 64, True), (4, 5, 32, False), (6, 1, 16, True)])
+def test_attention_inputs_small_heads(hip, dtype, heads, kv, dim, gated):
+    # value tiles of several key heads, the last tile's heads cut short
+    t, start = 37, 5
+    step(f"attentionInputs {dtype} heads {heads}/{kv} of {dim}, {t} tokens, gated {gated}")
+    pages = -(-(start + t) // PAGE) + 1
+    table = np.random.default_rng(dim).permutation(pages).astype(np.int32)
+    rope = d.Rope(1e4, dim, d.RopeLayout.Neox, d.RopeSections.Single())
+    run_attention_inputs(hip, dtype, t, heads, kv, dim, rope, start, table, pages, gated, 120 + dim)
+
+
 def test_attention_inputs_flag_a_page_outside_the_cache(hip):
     step("attentionInputs with a page-table entry past the cache")
     t, heads, kv, dim = 4, 4, 2, 128
