@@ -718,12 +718,16 @@ int64_t resident_waves(Kernel kernel) {
 template <int K, bool FULL>
 void adaln_resident_launch(const uint16_t* x, const float* scale, const float* shift, uint16_t* out, int64_t rows,
                            int cols, int64_t rows_per_sample, int64_t samples, float eps, hipStream_t s) {
-  // every wave resident at once, rows shared out as evenly as they go
-  static std::atomic<int64_t> budget{0};
-  int64_t waves = budget.load(std::memory_order_relaxed);
+  // every wave resident at once, rows shared out as evenly as they go; the
+  // residency is the current device's, found once per device
+  constexpr int kDevices = 64;
+  static std::atomic<int64_t> budget[kDevices] = {};
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= kDevices) device = 0;
+  int64_t waves = budget[device].load(std::memory_order_relaxed);
   if (waves == 0) {
     waves = std::max<int64_t>(resident_waves(adaln_resident<K, FULL>), 4);
-    budget.store(waves, std::memory_order_relaxed);
+    budget[device].store(waves, std::memory_order_relaxed);
   }
   int64_t per_sample = std::max<int64_t>(1, std::min(rows_per_sample, waves / samples));
   per_sample = ceil_div(rows_per_sample, ceil_div(rows_per_sample, per_sample));
