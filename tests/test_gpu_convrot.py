@@ -52,6 +52,7 @@ CASES = [
     ("int8 one scale", False, 0, True),
     ("4-bit groups of 16", True, 16, False),
     ("4-bit groups of 32", True, 32, False),
+    ("4-bit groups of 64", True, 64, False),
     ("4-bit groups of 128", True, 128, False),
     ("4-bit groups of 512", True, 512, False),
 ]
@@ -106,11 +107,14 @@ def test_codes_at_any_alignment(hip, four_bit, offset):
     same_bits(r.embedding(ids).view(np.uint32), host_f32(got).view(np.uint32), f"offset {offset} embedding")
 
 
-def test_nan_relative_scales_and_codebooks(hip):
+@pytest.mark.parametrize("group_size", [32, 64, 256])
+def test_nan_relative_scales_and_codebooks(hip, group_size):
     rows, cols = 6, 512
-    r = o.random_rotated(rows, cols, np.random.default_rng(61), True, 32)
-    r.relative[2, 3] = 0x7F  # row 2, first group of 256: NaN
-    r.relative[5, 15] = 0xFF  # row 5, second group
+    r = o.random_rotated(rows, cols, np.random.default_rng(61), True, group_size)
+    per_row = cols // group_size
+    r.relative[2, 3 * per_row // 16] = 0x7F  # row 2, first group of 256: NaN
+    r.relative[5, per_row - 1] = 0xFF  # row 5, second group
+    r.relative[4, 0] = 0x00  # a zero relative scale: an infinite entry's level is NaN
     table = device_table(hip, r)
     step("rotated dequantize with NaN relative scales")
     out = torch.empty((rows, cols), dtype=torch.bfloat16, device=DEV)
