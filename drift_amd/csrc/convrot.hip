@@ -18,10 +18,7 @@
 // Layout on the wave: four lanes a group of 256 values, a lane a quarter of
 // it (64 consecutive values, digits 0-2 in its registers, digit 3 its lane
 // in the quad), 16 groups a wave. A lane loads its codes with 16-byte loads
-// (64 B of int8, 32 B of nibbles), decodes (a 4-bit code's value comes from
-// the lane holding its codebook entry by ds_bpermute, or, where the lane's 64
-// values share one relative scale, from a 16-entry table of finished values
-// the lane writes to LDS), and runs the rounds of digits 0,
+// (64 B of int8, 32 B of nibbles), decodes, and runs the rounds of digits 0,
 // 1 and 2 in registers. The quad then trades values through the wave's own
 // LDS (4 KiB, a quarter of the values at a time), so that a lane holds digit
 // 3 and digits 0-1 for one digit 2; it runs the last round in registers and
@@ -75,13 +72,15 @@ __device__ __forceinline__ void round_of(float (&v)[kLaneValues]) {
 }
 
 // The codes of a lane's 64 values: `Bytes` bytes from p, in 16-byte loads
-// where p allows, byte loads where it does not.
+// where p allows, byte loads where it does not. Plain loads: a load
+// instruction here reads 16 bytes of every lane's 64 or 32, a part of each
+// line, and the non-temporal form measured 12-20% slower.
 template <int Bytes, bool ALIGNED>
 __device__ __forceinline__ void load_codes(const uint8_t* p, uint32_t (&w)[Bytes / 4]) {
   if constexpr (ALIGNED) {
 #pragma unroll
     for (int k = 0; k < Bytes / 16; ++k) {
-      const uint4 q = stream_load(p + 16 * k);
+      const uint4 q = *reinterpret_cast<const uint4*>(p + 16 * k);
       w[4 * k] = q.x;
       w[4 * k + 1] = q.y;
       w[4 * k + 2] = q.z;
@@ -158,17 +157,10 @@ struct Parts {
 // Rows ids[t] (row t with no ids) of a rotated weight [rows, cols] into out
 // [count, cols]; T float (the BF16 value widened, as the reference gathers)
 // or uint16_t (BF16). An id outside [0, rows) gets zeros and sets *bad_id.
-// A lane's 16 levels in LDS: 17 floats apart, so that lanes looking up one
-// code read 64 different banks.
-constexpr int kLevelStride = 17;
-
-// The table-lookup decode leaves room for five waves a SIMD (measured 7-9%
-// faster than four); the int8 decode measured slower at five.
-template <typename T, bool FOUR_BIT, bool ALIGNED, bool ONE_REL>
-__global__ void __launch_bounds__(kBlockWaves * kWave) __attribute__((amdgpu_waves_per_eu(ONE_REL ? 5 : 1, 8)))
+template <typename T, bool FOUR_BIT, bool ALIGNED>
+__global__ void __launch_bounds__(kBlockWaves * kWave)
     rotated_rows(Parts parts, const int32_t* ids, T* out, int64_t count, int64_t rows, int cols, int32_t* bad_id) {
   __shared__ float4 trade[kBlockWaves][kWaveGroups * 16];  // 4 KiB a wave
-  __shared__ float levels[ONE_REL ? kBlockWaves : 1][ONE_REL ? kWave * kLevelStride : 1];
   const int lane = (int)threadIdx.x % kWave, wave = (int)threadIdx.x / kWave;
   const int g = lane >> 2, q = lane & 3;  // group in the wave, quarter in the group
   const int per_row = cols / kGroup;
@@ -195,44 +187,28 @@ __global__ void __launch_bounds__(kBlockWaves * kWave) __attribute__((amdgpu_wav
     // ops/CpuBase.scala:50-66: the low nibble the even column; level =
     // clamp(rint(codebook(code) * relative), -127, 127), a NaN kept (Java's
     // min and max), times the row's scale.
+    const float entry = parts.codebook[lane & 15];
     uint32_t w[8];
     load_codes<32, ALIGNED>(parts.codes + row * (cols / 2) + first / 2, w);
     const int64_t rel_row = row * (cols / parts.group_size);
-    if constexpr (ONE_REL) {
-      // groups of a multiple of 64 columns: the lane's 64 values share one
-      // relative scale, so the lane makes its 16 values (one a code, NaN
-      // kept) into its own LDS slot and looks each code up there
-      const float rel = e4m3(parts.relative[rel_row + first / parts.group_size]);
-      float* mine = levels[wave] + lane * kLevelStride;
+    uint32_t rel_code[4];
 #pragma unroll
-      for (int c = 0; c < 16; ++c) {
-        const float p = parts.codebook[c] * rel;
-        mine[c] = (p != p ? p : fminf(fmaxf(__builtin_rintf(p), -127.0f), 127.0f)) * scale;
-      }
-      wave_sync();
+    for (int r = 0; r < 4; ++r) rel_code[r] = parts.relative[rel_row + (first + 16 * r) / parts.group_size];
+    float rel[4];
 #pragma unroll
-      for (int j = 0; j < kLaneValues; ++j) v[j] = mine[nibble_address(w, j) >> 2];
-    } else {
-      const float entry = parts.codebook[lane & 15];
-      uint32_t rel_code[4];
+    for (int r = 0; r < 4; ++r) rel[r] = e4m3(rel_code[r]);
+    // codes whose entry is NaN, or infinite (lanes 0-15 hold the 16 entries)
+    const uint32_t nan_codes = (uint32_t)__ballot(lane < 16 && entry != entry) & 0xffffu;
+    const uint32_t inf_codes = (uint32_t)__ballot(lane < 16 && __builtin_isinf(entry)) & 0xffffu;
+    uint32_t bad[4];
+    bool any = false;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) rel_code[r] = parts.relative[rel_row + (first + 16 * r) / parts.group_size];
-      float rel[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) rel[r] = e4m3(rel_code[r]);
-      // codes whose entry is NaN, or infinite (lanes 0-15 hold the 16 entries)
-      const uint32_t nan_codes = (uint32_t)__ballot(lane < 16 && entry != entry) & 0xffffu;
-      const uint32_t inf_codes = (uint32_t)__ballot(lane < 16 && __builtin_isinf(entry)) & 0xffffu;
-      uint32_t bad[4];
-      bool any = false;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        bad[r] = rel[r] != rel[r] ? 0xffffu : nan_codes | (rel[r] == 0.0f ? inf_codes : 0u);
-        any |= bad[r] != 0;
-      }
-      decode_nibbles(w, entry, rel, scale, v);
-      if (__any(any)) keep_nans(w, bad, v);
+    for (int r = 0; r < 4; ++r) {
+      bad[r] = rel[r] != rel[r] ? 0xffffu : nan_codes | (rel[r] == 0.0f ? inf_codes : 0u);
+      any |= bad[r] != 0;
     }
+    decode_nibbles(w, entry, rel, scale, v);
+    if (__any(any)) keep_nans(w, bad, v);
   }
 
   // digits 0, 1, 2 (strides 1, 4, 16) in registers
@@ -340,26 +316,18 @@ int rotated_launch(const char* entry, const Parts& parts, const int32_t* ids, T*
   const hipStream_t s = (hipStream_t)stream;
   const dim3 grid((unsigned)blocks), block(kBlockWaves * kWave);
   if (four_bit) {
-    const bool one_rel = parts.group_size % kLaneValues == 0;
-    if (aligned && one_rel)
-      hipLaunchKernelGGL((rotated_rows<T, true, true, true>), grid, block, 0, s, parts, ids, out, count, rows, cols,
-                         bad_id);
-    else if (aligned)
-      hipLaunchKernelGGL((rotated_rows<T, true, true, false>), grid, block, 0, s, parts, ids, out, count, rows, cols,
-                         bad_id);
-    else if (one_rel)
-      hipLaunchKernelGGL((rotated_rows<T, true, false, true>), grid, block, 0, s, parts, ids, out, count, rows, cols,
-                         bad_id);
+    if (aligned)
+      hipLaunchKernelGGL((rotated_rows<T, true, true>), grid, block, 0, s, parts, ids, out, count, rows, cols, bad_id);
     else
-      hipLaunchKernelGGL((rotated_rows<T, true, false, false>), grid, block, 0, s, parts, ids, out, count, rows,
-                         cols, bad_id);
+      hipLaunchKernelGGL((rotated_rows<T, true, false>), grid, block, 0, s, parts, ids, out, count, rows, cols,
+                         bad_id);
   } else {
     if (aligned)
-      hipLaunchKernelGGL((rotated_rows<T, false, true, false>), grid, block, 0, s, parts, ids, out, count, rows, cols,
+      hipLaunchKernelGGL((rotated_rows<T, false, true>), grid, block, 0, s, parts, ids, out, count, rows, cols,
                          bad_id);
     else
-      hipLaunchKernelGGL((rotated_rows<T, false, false, false>), grid, block, 0, s, parts, ids, out, count, rows,
-                         cols, bad_id);
+      hipLaunchKernelGGL((rotated_rows<T, false, false>), grid, block, 0, s, parts, ids, out, count, rows, cols,
+                         bad_id);
   }
   return launched(entry);
 }
