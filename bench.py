@@ -342,7 +342,7 @@ def host_cpu() -> str:
 
 def host_threads() -> int:
     """Host threads for the all-cores leg: this process's CPUs, at most 16
-    (one GPU's share of a GPU box's cores)."""
+    (one GPU's share of an 8-GPU node's host cores)."""
     return max(1, min(16, len(os.sched_getaffinity(0))))
 
 
