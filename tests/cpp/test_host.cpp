@@ -470,6 +470,219 @@ GPU_TEST(outputs_may_alias_their_inputs) {
   close_f32(want4, dev.download<float>(gd), "gated into its gate");
 }
 
+GPU_TEST(norms_modulation_and_residual_gates) {
+  HipOps hip;
+  Device dev;
+  const int64_t rows = 6, cols = 3072;
+  std::vector<float> x = gaussian(30, rows * cols), y = gaussian(31, rows * cols), w = gaussian(32, cols),
+                     b = gaussian(33, cols);
+  // addRmsNorm: x += y written back, then the norm of the sum
+  const Tensor xd = dev.upload(DType::F32, {rows, cols}, x), out = dev.empty(DType::F32, {rows, cols});
+  hip.addRmsNorm(xd, dev.upload(DType::F32, {rows, cols}, y), RowNorm{dev.upload(DType::F32, {cols}, w), 1e-6f, 0.0f, out});
+  std::vector<float> summed = x, want(x.size());
+  oracle_rms_norm(summed.data(), y.data(), w.data(), want.data(), rows, cols, 1e-6f, 0.0f, 1);
+  exact(summed, dev.download<float>(xd), "addRmsNorm x += y");
+  close_f32(want, dev.download<float>(out), "addRmsNorm");
+  // layerNorm with weight and bias, then modulate
+  const Tensor wd = dev.upload(DType::F32, {cols}, w), bd = dev.upload(DType::F32, {cols}, b);
+  const Tensor x2 = dev.upload(DType::F32, {rows, cols}, x), ln = dev.empty(DType::F32, {rows, cols});
+  hip.layerNorm(x2, &wd, &bd, 1e-5f, ln);
+  std::vector<float> want_ln(x.size());
+  oracle_layer_norm(x.data(), w.data(), b.data(), want_ln.data(), rows, cols, 1e-5f);
+  close_f32(want_ln, dev.download<float>(ln), "layerNorm");
+  const Tensor mod = dev.empty(DType::F32, {rows, cols});
+  hip.modulate(x2, wd, bd, mod);
+  std::vector<float> want_mod(x.size());
+  oracle_modulate(x.data(), w.data(), b.data(), want_mod.data(), rows, cols);
+  close_f32(want_mod, dev.download<float>(mod), "modulate");
+  // per-row chunk tables: modulateChunks, gatedAddChunk, rowGatedAdd
+  const int chunks = 6;
+  std::vector<float> table = gaussian(34, rows * chunks * cols, 0.1f), g = gaussian(35, rows);
+  const Tensor td = dev.upload(DType::F32, {rows, chunks * cols}, table);
+  const Tensor mc = dev.empty(DType::F32, {rows, cols});
+  hip.modulateChunks(x2, td, 3, 4, mc);
+  std::vector<float> want_mc(x.size());
+  oracle_modulate_chunks(x.data(), table.data(), want_mc.data(), rows, cols, chunks, 3, 4);
+  close_f32(want_mc, dev.download<float>(mc), "modulateChunks");
+  const Tensor x3 = dev.upload(DType::F32, {rows, cols}, x), yd = dev.upload(DType::F32, {rows, cols}, y);
+  hip.gatedAddChunk(x3, yd, td, 5);
+  std::vector<float> want_gc = x;
+  oracle_gated_add_chunk(want_gc.data(), y.data(), table.data(), rows, cols, chunks, 5);
+  close_f32(want_gc, dev.download<float>(x3), "gatedAddChunk");
+  const Tensor x4 = dev.upload(DType::F32, {rows, cols}, x);
+  hip.rowGatedAdd(x4, yd, dev.upload(DType::F32, {rows}, g));
+  std::vector<float> want_rg = x;
+  oracle_row_gated_add(want_rg.data(), y.data(), g.data(), rows, cols);
+  close_f32(want_rg, dev.download<float>(x4), "rowGatedAdd");
+}
+
+GPU_TEST(quantize_and_scaled_activation) {
+  HipOps hip;
+  Device dev;
+  const int64_t blocks = 515;
+  std::vector<float> x = gaussian(36, blocks * 32, 2.0f);
+  std::vector<int8_t> codes0(blocks * 32);
+  const Tensor xd = dev.upload(DType::F32, {blocks * 32}, x);
+  const Tensor codes = dev.upload(DType::I8, {blocks * 32}, codes0);
+  const Tensor scales = dev.empty(DType::F32, {blocks}), sums = dev.empty(DType::F32, {blocks});
+  hip.quantize(xd, blocks, QuantizedOutput{codes.data, static_cast<float*>(scales.data), static_cast<float*>(sums.data)});
+  std::vector<int8_t> want_codes(blocks * 32);
+  std::vector<float> want_scales(blocks), want_sums(blocks);
+  oracle_quantize_x(x.data(), want_codes.data(), want_scales.data(), want_sums.data(), blocks);
+  exact(want_codes, dev.download<int8_t>(codes), "quantize codes");
+  exact(want_scales, dev.download<float>(scales), "quantize scales");
+  exact(want_sums, dev.download<float>(sums), "quantize sums");
+  const Tensor out = dev.empty(DType::F32, {blocks * 32});
+  hip.scaledActivation(Activation::GeluErf, 0.5f, xd, out);
+  std::vector<float> want(x.size());
+  oracle_activation(2, 0.5f, x.data(), want.data(), (int64_t)x.size());
+  close_f32(want, dev.download<float>(out), "scaledActivation GELU-erf");
+}
+
+GPU_TEST(rope_tables_and_wan_3d) {
+  HipOps hip;
+  Device dev;
+  const int tokens = 9, heads = 3, dim = 128, pairs = 48;
+  std::vector<float> x = gaussian(37, (size_t)tokens * heads * dim), c(tokens * pairs), sn(tokens * pairs);
+  for (int i = 0; i < tokens * pairs; ++i) {
+    c[i] = std::cos(0.01f * (float)i);
+    sn[i] = std::sin(0.01f * (float)i);
+  }
+  const Tensor xd = dev.upload(DType::F32, {tokens, heads, dim}, x), out = dev.empty(DType::F32, {tokens, heads, dim});
+  hip.ropeTable(xd, dev.upload(DType::F32, {tokens, pairs}, c), dev.upload(DType::F32, {tokens, pairs}, sn), out, true);
+  std::vector<float> want(x.size());
+  oracle_rope_table(x.data(), c.data(), sn.data(), want.data(), tokens, heads, dim, pairs, 0, 1);
+  close_f32(want, dev.download<float>(out), "ropeTable halves");
+  // Wan's 3-D grid 2 x 3 x 5, in place on bf16
+  const int frames = 2, grid_rows = 3, grid_cols = 5, wan_tokens = frames * grid_rows * grid_cols;
+  std::vector<uint16_t> xb = to_bf16(gaussian(38, (size_t)wan_tokens * 2 * dim));
+  const Tensor wd = dev.upload(DType::BF16, {wan_tokens, 2, dim}, xb);
+  hip.rope3d(wd, frames, grid_rows, grid_cols, wd);
+  std::vector<float> wc((size_t)wan_tokens * dim / 2), ws(wc.size()), xf = from_bf16(xb), wwant(xf.size());
+  oracle_wan_angles(frames, grid_rows, grid_cols, dim, 10000.0, wc.data(), ws.data());
+  oracle_rope_table(xf.data(), wc.data(), ws.data(), wwant.data(), wan_tokens, 2, dim, dim / 2, 0, 0);
+  within_ulp(to_bf16(wwant), dev.download<uint16_t>(wd), "rope3d bf16 in place");
+}
+
+GPU_TEST(query_key_norm_rope_f32) {
+  HipOps hip;
+  Device dev;
+  const int tokens = 11, qh = 4, kh = 2, dim = 128;
+  std::vector<float> q = gaussian(39, (size_t)tokens * qh * dim, 2.0f), k = gaussian(40, (size_t)tokens * kh * dim, 2.0f);
+  std::vector<float> qw = gaussian(41, dim, 0.1f), kw = gaussian(42, dim, 0.1f);
+  for (float& v : qw) v += 1.0f;
+  for (float& v : kw) v += 1.0f;
+  std::vector<int32_t> positions(tokens);
+  for (int t = 0; t < tokens; ++t) positions[t] = 100 + 7 * t;
+  const Rope rope{1e6f, dim, RopeLayout::Neox, {}};
+  const QueryKeyNorms norms{dev.upload(DType::F32, {dim}, qw), dev.upload(DType::F32, {dim}, kw), 1e-6f, 0.0f, rope};
+  const Tensor rq = dev.empty(DType::F32, {tokens, qh, dim}), rk = dev.empty(DType::F32, {tokens, kh, dim});
+  hip.queryKeyNormRope(dev.upload(DType::F32, {tokens, qh, dim}, q), dev.upload(DType::F32, {tokens, kh, dim}, k),
+                       norms, dev.upload(DType::I32, {tokens}, positions), rq, rk);
+  // the reference's composition: rmsNorm per head (F32 written), then rope
+  const int32_t s[4] = {0, 0, 0, 0};
+  auto composed = [&](std::vector<float> v, const std::vector<float>& w, int heads) {
+    std::vector<float> normed(v.size()), rotated(v.size());
+    oracle_rms_norm(v.data(), nullptr, w.data(), normed.data(), (int64_t)tokens * heads, dim, 1e-6f, 0.0f, 1);
+    oracle_rope(normed.data(), positions.data(), rotated.data(), tokens, heads, dim, dim, 1e6f, 0, 0, s);
+    return rotated;
+  };
+  close_f32(composed(q, qw, qh), dev.download<float>(rq), "queryKeyNormRope queries");
+  close_f32(composed(k, kw, kh), dev.download<float>(rk), "queryKeyNormRope keys");
+}
+
+GPU_TEST(attention_inputs_equal_their_steps) {
+  // the fused gated step against split, norms + rope and the cache write
+  // launched one by one (FusedOpsTests.scala:406-499 asks the same), in F32:
+  // with BF16 the steps would round the turned keys to BF16 before F16
+  HipOps hip;
+  Device dev;
+  const int tokens = 21, qh = 8, kh = 2, dim = 128, page = 16, pages = 4;
+  const int64_t start = 5;
+  std::vector<float> qg = gaussian(43, (size_t)tokens * qh * 2 * dim, 2.0f);
+  std::vector<float> k = gaussian(44, (size_t)tokens * kh * dim, 2.0f);
+  std::vector<float> v = gaussian(45, (size_t)tokens * kh * dim);
+  std::vector<float> w = gaussian(46, dim, 0.1f);
+  for (float& x : w) x += 1.0f;
+  std::vector<int32_t> positions(tokens), table = {2, 0, 3, 1};
+  for (int t = 0; t < tokens; ++t) positions[t] = (int32_t)start + t;
+  std::vector<uint16_t> blank((size_t)pages * page * kh * dim, 0);
+  const Tensor wd = dev.upload(DType::F32, {dim}, w);
+  const QueryKeyNorms norms{wd, wd, 1e-6f, 0.0f, Rope{1e6f, dim, RopeLayout::Neox, {}}};
+  const Tensor qgd = dev.upload(DType::F32, {tokens, qh, 2 * dim}, qg), kd = dev.upload(DType::F32, {tokens, kh, dim}, k);
+  const Tensor vd = dev.upload(DType::F32, {tokens, kh, dim}, v), pos = dev.upload(DType::I32, {tokens}, positions);
+  const Tensor pt = dev.upload(DType::I32, {pages}, table);
+  auto make_cache = [&] {
+    return KvCache::of(dev.upload(DType::F16, {pages, page, kh, dim}, blank),
+                       dev.upload(DType::F16, {pages, kh, dim, page}, blank), page);
+  };
+  // fused
+  const KvCache fused_cache = make_cache();
+  const Tensor queries = dev.empty(DType::F32, {tokens, qh, dim}), gate = dev.empty(DType::F32, {tokens, qh, dim});
+  const Tensor rkeys = dev.empty(DType::F32, {tokens, kh, dim}), rq = dev.empty(DType::F32, {tokens, qh, dim});
+  hip.attentionInputs(qgd, kd, vd, norms, pos, fused_cache, pt, start, queries, gate, rkeys, rq);
+  // step by step
+  const KvCache steps_cache = make_cache();
+  const Tensor q2 = dev.empty(DType::F32, {tokens, qh, dim}), g2 = dev.empty(DType::F32, {tokens, qh, dim});
+  const Tensor rq2 = dev.empty(DType::F32, {tokens, qh, dim}), rk2 = dev.empty(DType::F32, {tokens, kh, dim});
+  hip.splitHalves(qgd, q2, g2);
+  hip.queryKeyNormRope(q2, kd, norms, pos, rq2, rk2);
+  hip.cacheWrite(rk2, vd, steps_cache, pt, start);
+  exact(dev.download<float>(g2), dev.download<float>(gate), "the gate half");
+  exact(dev.download<float>(rq2), dev.download<float>(rq), "rotated queries");
+  exact(dev.download<uint16_t>(steps_cache.keys), dev.download<uint16_t>(fused_cache.keys), "cached keys");
+  exact(dev.download<uint16_t>(steps_cache.values), dev.download<uint16_t>(fused_cache.values), "cached values");
+  // queryKeyNormRopeCache: the same without the gate
+  const KvCache nogate_cache = make_cache();
+  const Tensor rq3 = dev.empty(DType::F32, {tokens, qh, dim});
+  hip.queryKeyNormRopeCache(q2, kd, vd, norms, pos, nogate_cache, pt, start, rq3);
+  exact(dev.download<float>(rq2), dev.download<float>(rq3), "queryKeyNormRopeCache queries");
+  exact(dev.download<uint16_t>(steps_cache.keys), dev.download<uint16_t>(nogate_cache.keys), "queryKeyNormRopeCache keys");
+}
+
+GPU_TEST(stored_and_rotated_tables) {
+  HipOps hip;
+  Device dev;
+  // Q4_K: the whole table decoded to BF16, bit-exact
+  const StorageType& q4k = StorageType::named("Q4_K");
+  const int64_t rows = 12, cols = 512, row_bytes = q4k.rowBytes(cols);
+  std::mt19937_64 rng(47);
+  std::vector<uint8_t> bytes((size_t)(rows * row_bytes));
+  for (auto& b : bytes) b = (uint8_t)rng();
+  for (int64_t blk = 0; blk < rows * cols / 256; ++blk) {  // finite d and dmin
+    const uint16_t d = oracle_f32_to_f16(1e-3f * (float)(1 + rng() % 100)),
+                   dm = oracle_f32_to_f16(1e-3f * (float)(1 + rng() % 100));
+    std::memcpy(&bytes[(size_t)(blk * 144)], &d, 2);
+    std::memcpy(&bytes[(size_t)(blk * 144 + 2)], &dm, 2);
+  }
+  const StoredTable t{dev.upload(DType::U8, {rows, row_bytes}, bytes), &q4k, cols};
+  const Tensor out = dev.empty(DType::BF16, {rows, cols});
+  hip.dequantize(t, out);
+  std::vector<float> want((size_t)(rows * cols));
+  for (int64_t r = 0; r < rows; ++r)
+    expect(oracle_decode_row(q4k.ggmlId, bytes.data() + r * row_bytes, cols, want.data() + r * cols) == 0, "decode");
+  exact(to_bf16(want), dev.download<uint16_t>(out), "Q4_K dequantize");
+  // an int8 rotated weight gathered to F32 (the BF16 value widened)
+  const int64_t rr = 7, rc = 512;
+  std::vector<int8_t> codes((size_t)(rr * rc));
+  for (auto& c : codes) c = (int8_t)(rng() % 255 - 127);
+  std::vector<float> scales(rr);
+  for (auto& s : scales) s = 1e-3f * (float)(1 + rng() % 10);
+  const RotatedTable w = hip.rotated(dev.upload(DType::I8, {rr, rc}, codes), ConvRotParts{dev.upload(DType::F32, {rr}, scales), {}});
+  std::vector<int32_t> ids = {6, 0, 3, 3};
+  const Tensor got = dev.empty(DType::F32, {4, rc});
+  hip.embedding(w, dev.upload(DType::I32, {4}, ids), got);
+  std::vector<float> want_rows((size_t)(4 * rc));
+  expect(oracle_convrot_embedding(reinterpret_cast<const uint8_t*>(codes.data()), scales.data(), rr, nullptr, nullptr,
+                                  0, rr, rc, ids.data(), 4, want_rows.data()) == -1, "ids in range");
+  exact(want_rows, dev.download<float>(got), "rotated embedding");
+  // F32 -> BF16
+  std::vector<float> x = gaussian(48, 1000, 5.0f);
+  const Tensor xb = dev.empty(DType::BF16, {1000});
+  hip.convert(dev.upload(DType::F32, {1000}, x), xb);
+  exact(to_bf16(x), dev.download<uint16_t>(xb), "convert F32 to BF16");
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
