@@ -6,6 +6,8 @@
 #include <numeric>
 #include <sstream>
 
+#include <hip/hip_runtime_api.h>
+
 #include "../../include/drift_kernels.h"
 
 namespace drift {
@@ -299,9 +301,80 @@ HipOps::HipOps(void* stream) : stream_(stream) {
                                   DRIFT_ABI_VERSION));
 }
 
+HipOps::~HipOps() {
+  if (quantizedBuffer_) (void)hipFree(quantizedBuffer_);
+  if (scratch_) (void)hipFree(scratch_);
+}
+
 void HipOps::launched(const char* entry, int code) {
   ++writes_;
   if (code != 0) throw HipException(entry, code, drift_last_error());
+}
+
+// ---- the int8 side output's bookkeeping
+
+namespace {
+// Device memory of at least `bytes` in *buffer (grown, never shrunk).
+void ensure(void*& buffer, size_t& size, size_t bytes) {
+  if (size >= bytes) return;
+  if (buffer) (void)hipFree(buffer);
+  buffer = nullptr;
+  size = 0;
+  const size_t want = std::max<size_t>(bytes, 65536);
+  const hipError_t status = hipMalloc(&buffer, want);
+  if (status != hipSuccess) throw HipException("hipMalloc", (int)status, hipGetErrorString(status));
+  size = want;
+}
+}  // namespace
+
+QuantizedOutput HipOps::QuantizedValues::at(int64_t first) const {
+  float* scales = reinterpret_cast<float*>(codes + values);
+  float* sums = scales + values / 32;
+  return QuantizedOutput{codes + first, scales + first / 32, sums + first / 32};
+}
+
+const QuantizedOutput* HipOps::quantizedTarget(const Tensor& out, int64_t cols, const QuantizedOutput* given,
+                                               QuantizedOutput& owned, std::optional<QuantizedValues>& target) {
+  target.reset();
+  if (given) return given;
+  const int64_t values = out.elementCount();
+  if (!(quantizesX_ && out.dtype == DType::F32 && values <= QuantizedMaximumValues && cols % 32 == 0)) return nullptr;
+  ensure(quantizedBuffer_, quantizedBytes_, (size_t)(values + 8 * (values / 32)));
+  target = QuantizedValues{reinterpret_cast<uintptr_t>(out.data), values, static_cast<int8_t*>(quantizedBuffer_), 0};
+  owned = target->at(0);
+  return &owned;
+}
+
+void HipOps::wroteQuantized(const std::optional<QuantizedValues>& target) {
+  if (!target) return;
+  quantized_ = *target;
+  quantized_->written = writes_;
+}
+
+std::optional<QuantizedOutput> HipOps::quantizedInput(const Tensor& x, int64_t m, int64_t k) const {
+  if (!quantized_ || quantized_->written != writes_ || x.dtype != DType::F32) return std::nullopt;
+  const auto address = reinterpret_cast<uintptr_t>(x.data);
+  if (address < quantized_->address) return std::nullopt;
+  const uintptr_t bytes = address - quantized_->address;
+  const int64_t first = (int64_t)(bytes / 4);
+  if (bytes % (4 * 32) != 0 || k % 32 != 0 || first + m * k > quantized_->values) return std::nullopt;
+  return quantized_->at(first);
+}
+
+QuantizedOutput HipOps::quantize(const Tensor& x, int64_t m, int64_t k) {
+  quantizesX_ = true;
+  require((x.dtype == DType::F32 || x.dtype == DType::BF16) && (m * k) % 32 == 0 && x.elementCount() >= m * k,
+          text("quantize: ", m, " rows of ", k, " from ", x.shape.str()));
+  const int64_t values = m * k, blocks = values / 32;
+  ensure(scratch_, scratchBytes_, (size_t)(values + 8 * blocks));
+  const QuantizedOutput into = QuantizedValues{0, values, static_cast<int8_t*>(scratch_), 0}.at(0);
+  quantizeTo(x, blocks, into);
+  return into;
+}
+
+QuantizedOutput HipOps::productInput(const Tensor& x, int64_t m, int64_t k) {
+  if (const std::optional<QuantizedOutput> found = quantizedInput(x, m, k)) return *found;
+  return quantize(x, m, k);
 }
 
 // ---- norms
@@ -325,13 +398,21 @@ void HipOps::normRows(const Tensor& x, const Tensor* y, const Tensor& weight, fl
 void HipOps::rmsNorm(const Tensor& x, const Tensor& weight, float epsilon, float weightOffset, const Tensor& out,
                      const QuantizedOutput* quantized) {
   const int64_t rows = checkRowWise("rmsNorm", x, out, {&weight});
-  normRows(x, nullptr, weight, epsilon, weightOffset, out, rows, quantized);
+  QuantizedOutput owned;
+  std::optional<QuantizedValues> target;
+  const QuantizedOutput* q = quantizedTarget(out, out.shape.last(), quantized, owned, target);
+  normRows(x, nullptr, weight, epsilon, weightOffset, out, rows, q);
+  wroteQuantized(target);
 }
 
 void HipOps::addRmsNorm(const Tensor& x, const Tensor& y, const RowNorm& norm, const QuantizedOutput* quantized) {
   checkElementwise("addRmsNorm", {&x, &y});
   const int64_t rows = checkRowWise("addRmsNorm", x, norm.out, {&norm.weight});
-  normRows(x, &y, norm.weight, norm.epsilon, norm.weightOffset, norm.out, rows, quantized);
+  QuantizedOutput owned;
+  std::optional<QuantizedValues> target;
+  const QuantizedOutput* q = quantizedTarget(norm.out, norm.out.shape.last(), quantized, owned, target);
+  normRows(x, &y, norm.weight, norm.epsilon, norm.weightOffset, norm.out, rows, q);
+  wroteQuantized(target);
 }
 
 void HipOps::layerNorm(const Tensor& x, const Tensor* weight, const Tensor* bias, float epsilon, const Tensor& out) {
@@ -379,7 +460,7 @@ void HipOps::layerNormModulate(const Tensor& x, const Tensor& scale, const Tenso
                                            (int32_t)cols, per, epsilon, stream_));
 }
 
-void HipOps::quantize(const Tensor& x, int64_t blocks, const QuantizedOutput& into) {
+void HipOps::quantizeTo(const Tensor& x, int64_t blocks, const QuantizedOutput& into) {
   require((x.dtype == DType::F32 || x.dtype == DType::BF16) && blocks * 32 <= x.elementCount(),
           text("quantize: ", blocks, " blocks of 32 from ", x.shape.str()));
   int8_t* xq = static_cast<int8_t*>(into.codes);
@@ -470,8 +551,11 @@ void HipOps::scaledActivation(Activation kind, float inputScale, const Tensor& x
 }
 
 void HipOps::gated(Activation kind, const Tensor& gate, const Tensor& up, const Tensor& out,
-                   const QuantizedOutput* q) {
+                   const QuantizedOutput* quantized) {
   checkElementwise("gated", {&gate, &up, &out});
+  QuantizedOutput owned;
+  std::optional<QuantizedValues> target;
+  const QuantizedOutput* q = quantizedTarget(out, out.shape.last(), quantized, owned, target);
   int8_t* xq = q ? static_cast<int8_t*>(q->codes) : nullptr;
   float* xd = q ? q->scales : nullptr;
   float* xs = q ? q->sums : nullptr;
@@ -481,6 +565,7 @@ void HipOps::gated(Activation kind, const Tensor& gate, const Tensor& up, const 
   else
     launched("drift_gated_f32", drift_gated_f32(at<float>(gate), at<float>(up), at<float>(out), gate.elementCount(),
                                                  (int32_t)kind, xq, xd, xs, stream_));
+  wroteQuantized(target);
 }
 
 // ---- rotary

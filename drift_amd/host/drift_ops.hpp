@@ -14,8 +14,10 @@
 // Storage.Device); `out` is written, never read, and may be an input of the
 // elementwise and row-wise operations. Beyond the reference's F32 kernels the
 // operations take BF16 tensors with F32 norm, modulation and rope vectors.
-// Everything launches asynchronously on the stream given to the constructor;
-// nothing synchronizes and nothing is allocated.
+// Everything launches asynchronously on the stream given to the constructor
+// and nothing synchronizes. Nothing is allocated either, except the buffers
+// of the int8 side output's bookkeeping (below), which this object owns, as
+// the reference's backend owns its own (ops/HipBase.scala:148-183).
 #pragma once
 
 #include <cstdint>
@@ -218,6 +220,9 @@ class HipOps {
 
   // `stream`: a hipStream_t, null for the default stream.
   explicit HipOps(void* stream = nullptr);
+  ~HipOps();
+  HipOps(const HipOps&) = delete;
+  HipOps& operator=(const HipOps&) = delete;
 
   // Launches so far (ops/HipBase.scala:128-147 counts them for the int8 side
   // output's freshness).
@@ -233,8 +238,24 @@ class HipOps {
   // scale and shift ([samples, C]) over rows [s * rowsPerSample, ...).
   void layerNormModulate(const Tensor& x, const Tensor& scale, const Tensor& shift, float epsilon, const Tensor& out,
                          int64_t rowsPerSample = 0);
-  // quantize_x: `blocks` blocks of 32 values of x (ops/HipLinear.scala:366-386)
-  void quantize(const Tensor& x, int64_t blocks, const QuantizedOutput& into);
+  // quantize_x: `blocks` blocks of 32 values of x into the caller's buffers
+  void quantizeTo(const Tensor& x, int64_t blocks, const QuantizedOutput& into);
+
+  // ---- the int8 side output's bookkeeping (ops/HipBase.scala:117-214,
+  // ops/HipLinear.scala:142-143,366-386). Once int8 products run (the first
+  // `quantize`), rmsNorm, addRmsNorm and gated quantize an F32 output of at
+  // most QuantizedMaximumValues values (rows of a multiple of 32) as they
+  // write it, into a buffer this object owns, unless the caller passes its
+  // own QuantizedOutput. The buffers stay valid until the next call that
+  // writes them.
+  static constexpr int64_t QuantizedMaximumValues = 8 * 16384;
+  bool quantizesX() const { return quantizesX_; }
+  // `m` rows of x (`k` wide) as the last launch wrote them quantized, if it did
+  std::optional<QuantizedOutput> quantizedInput(const Tensor& x, int64_t m, int64_t k) const;
+  // `m` rows of x quantized now, into this object's scratch
+  QuantizedOutput quantize(const Tensor& x, int64_t m, int64_t k);
+  // what an int8 product over `m` rows of x reads: quantizedInput, else quantize
+  QuantizedOutput productInput(const Tensor& x, int64_t m, int64_t k);
 
   // ---- gated residuals (ops/ElementwiseOps.scala:28-92)
   void gatedAdd(const Tensor& x, const Tensor& y, const Tensor& gate, int64_t rowsPerSample = 0);
@@ -282,6 +303,26 @@ class HipOps {
  private:
   void* stream_;
   int64_t writes_ = 0;
+
+  // values at `address` a launch also wrote quantized at `codes` (codes, then
+  // scales, then sums), as of launch `written`
+  struct QuantizedValues {
+    uintptr_t address = 0;
+    int64_t values = 0;
+    int8_t* codes = nullptr;
+    int64_t written = 0;
+    QuantizedOutput at(int64_t first) const;
+  };
+  bool quantizesX_ = false;
+  std::optional<QuantizedValues> quantized_;
+  void* quantizedBuffer_ = nullptr;
+  size_t quantizedBytes_ = 0;
+  void* scratch_ = nullptr;
+  size_t scratchBytes_ = 0;
+
+  const QuantizedOutput* quantizedTarget(const Tensor& out, int64_t cols, const QuantizedOutput* given,
+                                         QuantizedOutput& owned, std::optional<QuantizedValues>& target);
+  void wroteQuantized(const std::optional<QuantizedValues>& target);
 
   void launched(const char* entry, int code);
   void normRows(const Tensor& x, const Tensor* y, const Tensor& weight, float epsilon, float weightOffset,

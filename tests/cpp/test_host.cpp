@@ -12,6 +12,8 @@
 #include <cstdio>
 #include <cstring>
 #include <functional>
+#include <optional>
+#include <tuple>
 #include <random>
 #include <string>
 #include <vector>
@@ -525,7 +527,7 @@ GPU_TEST(quantize_and_scaled_activation) {
   const Tensor xd = dev.upload(DType::F32, {blocks * 32}, x);
   const Tensor codes = dev.upload(DType::I8, {blocks * 32}, codes0);
   const Tensor scales = dev.empty(DType::F32, {blocks}), sums = dev.empty(DType::F32, {blocks});
-  hip.quantize(xd, blocks, QuantizedOutput{codes.data, static_cast<float*>(scales.data), static_cast<float*>(sums.data)});
+  hip.quantizeTo(xd, blocks, QuantizedOutput{codes.data, static_cast<float*>(scales.data), static_cast<float*>(sums.data)});
   std::vector<int8_t> want_codes(blocks * 32);
   std::vector<float> want_scales(blocks), want_sums(blocks);
   oracle_quantize_x(x.data(), want_codes.data(), want_scales.data(), want_sums.data(), blocks);
@@ -681,6 +683,56 @@ GPU_TEST(stored_and_rotated_tables) {
   const Tensor xb = dev.empty(DType::BF16, {1000});
   hip.convert(dev.upload(DType::F32, {1000}, x), xb);
   exact(to_bf16(x), dev.download<uint16_t>(xb), "convert F32 to BF16");
+}
+
+// ops/HipBase.scala:117-214 and FusedOpsTests.scala:96-176: once int8
+// products run, the F32 norm and `gated` write their output quantized too,
+// the same as quantizing it afterwards; any launch after makes it stale.
+GPU_TEST(the_int8_side_output_bookkeeping) {
+  HipOps hip;
+  Device dev;
+  const int64_t rows = 4, cols = 4096;
+  std::vector<float> x = gaussian(50, rows * cols, 2.0f), w = gaussian(51, cols, 0.1f);
+  for (float& v : w) v += 1.0f;
+  const Tensor xd = dev.upload(DType::F32, {rows, cols}, x), wd = dev.upload(DType::F32, {cols}, w);
+  const Tensor out = dev.empty(DType::F32, {rows, cols});
+  hip.rmsNorm(xd, wd, 1e-6f, 0.0f, out);
+  expect(!hip.quantizesX() && !hip.quantizedInput(out, rows, cols), "no side output before int8 products run");
+  hip.quantize(xd, rows, cols);  // the first int8 product
+  expect(hip.quantizesX(), "quantize marks that int8 products run");
+  hip.rmsNorm(xd, wd, 1e-6f, 0.0f, out);
+  const std::optional<QuantizedOutput> side = hip.quantizedInput(out, rows, cols);
+  expect(side.has_value(), "the norm wrote its output quantized");
+  auto grab = [&](const QuantizedOutput& q, int64_t values) {
+    std::vector<int8_t> codes((size_t)values);
+    std::vector<float> scales((size_t)(values / 32)), sums((size_t)(values / 32));
+    hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize");
+    hip_check(hipMemcpy(codes.data(), q.codes, codes.size(), hipMemcpyDeviceToHost), "hipMemcpy");
+    hip_check(hipMemcpy(scales.data(), q.scales, scales.size() * 4, hipMemcpyDeviceToHost), "hipMemcpy");
+    hip_check(hipMemcpy(sums.data(), q.sums, sums.size() * 4, hipMemcpyDeviceToHost), "hipMemcpy");
+    return std::make_tuple(codes, scales, sums);
+  };
+  const auto written = grab(*side, rows * cols);
+  // rows 2-3 alone: the same blocks, from where they start
+  const Tensor tail{DType::F32, {2, cols}, static_cast<float*>(out.data) + 2 * cols};
+  const auto tail_side = grab(*hip.quantizedInput(tail, 2, cols), 2 * cols);
+  expect(std::equal(std::get<0>(tail_side).begin(), std::get<0>(tail_side).end(),
+                    std::get<0>(written).begin() + 2 * cols), "rows 2-3 of the side output");
+  const auto fresh = grab(hip.quantize(out, rows, cols), rows * cols);
+  exact(std::get<0>(fresh), std::get<0>(written), "side output codes");
+  exact(std::get<1>(fresh), std::get<1>(written), "side output scales");
+  exact(std::get<2>(fresh), std::get<2>(written), "side output sums");
+  expect(!hip.quantizedInput(out, rows, cols), "a launch after the norm makes its side output stale");
+  // gated writes its output quantized too; productInput finds it
+  std::vector<float> g = gaussian(52, rows * cols), u = gaussian(53, rows * cols);
+  const Tensor gout = dev.empty(DType::F32, {rows, cols});
+  hip.gated(Activation::Silu, dev.upload(DType::F32, {rows, cols}, g), dev.upload(DType::F32, {rows, cols}, u), gout);
+  const int64_t before = hip.deviceWrites();
+  const auto product = grab(hip.productInput(gout, rows, cols), rows * cols);
+  expect(hip.deviceWrites() == before, "productInput read the side output without a launch");
+  const auto requantized = grab(hip.quantize(gout, rows, cols), rows * cols);
+  exact(std::get<0>(requantized), std::get<0>(product), "gated side output codes");
+  exact(std::get<1>(requantized), std::get<1>(product), "gated side output scales");
 }
 
 }  // namespace
