@@ -314,7 +314,9 @@ class _Reader:
             return
         offsets = (16, 17) if t.dtype.name == "Q4_0_ROCMFP4" else (16,)
         blocks = min(t.byteSize // t.dtype.bytes, _ROCM_SAMPLED_BLOCKS)
-        data = np.frombuffer(self.b, np.uint8, blocks * t.dtype.bytes, t.fileOffset).reshape(blocks, -1)
+        # a copy: a view left on the mapping would keep a refused file's
+        # mapping from closing
+        data = np.frombuffer(self.b, np.uint8, blocks * t.dtype.bytes, t.fileOffset).reshape(blocks, -1).copy()
         scales = data[:, list(offsets)]
         bad = np.flatnonzero(scales.reshape(-1) > 0x7E)  # the first in byte order, as the reference scans
         if bad.size:

@@ -19,6 +19,7 @@
 #include <vector>
 
 #include "../../drift_amd/host/drift_ops.hpp"
+#include "../../drift_amd/host/gguf.hpp"
 #include "../../oracle/cpu_ops.h"
 #include "comparison.hpp"
 
@@ -737,7 +738,51 @@ GPU_TEST(the_int8_side_output_bookkeeping) {
 
 }  // namespace
 
+// --gguf FILE...: each file as the C++ reader sees it, one line a fact
+// (version and alignment, then each tensor by name, then each unsupported
+// one), or the refusal; tests/test_cpp_host.py holds it to the Python reader.
+int summarize_gguf(int count, char** paths) {
+  for (int i = 0; i < count; ++i) {
+    std::printf("file %s\n", paths[i]);
+    try {
+      const gguf::File f = gguf::File::open(paths[i]);
+      std::printf("version %d alignment %lld\n", f.version(), (long long)f.alignment());
+      for (const auto& [name, t] : f.tensors()) {
+        std::string shape;
+        for (int64_t d : t.shape) shape += (shape.empty() ? "" : ",") + std::to_string(d);
+        std::printf("tensor %s %s [%s] %lld %lld\n", name.c_str(), t.type->name, shape.c_str(),
+                    (long long)t.fileOffset, (long long)t.byteSize());
+      }
+      for (const auto& [name, reason] : f.unsupported()) std::printf("unsupported %s: %s\n", name.c_str(), reason.c_str());
+    } catch (const gguf::FormatError& e) {
+      std::printf("refused %s\n", e.what());
+    }
+  }
+  return 0;
+}
+
+// --gguf-embed FILE NAME ID...: the table NAME gathered to F32 on the GPU at
+// the ids, printed as one FNV-1a hash of the output's bytes.
+int embed_gguf(int argc, char** argv) {
+  const gguf::File f = gguf::File::open(argv[0]);
+  const gguf::DeviceTable t = f.table(argv[1]);
+  std::vector<int32_t> ids;
+  for (int i = 2; i < argc; ++i) ids.push_back(std::atoi(argv[i]));
+  HipOps hip;
+  Device dev;
+  const int64_t cols = t.table().cols, count = (int64_t)ids.size();
+  const Tensor out = dev.empty(DType::F32, {count, cols});
+  hip.embedding(t.table(), dev.upload(DType::I32, {count}, ids), out);
+  const std::vector<uint8_t> bytes = dev.download<uint8_t>(out);
+  uint64_t h = 1469598103934665603ull;
+  for (uint8_t b : bytes) h = (h ^ b) * 1099511628211ull;
+  std::printf("embedding %llu\n", (unsigned long long)h);
+  return 0;
+}
+
 int main(int argc, char** argv) {
+  if (argc > 1 && std::string(argv[1]) == "--gguf") return summarize_gguf(argc - 2, argv + 2);
+  if (argc > 3 && std::string(argv[1]) == "--gguf-embed") return embed_gguf(argc - 2, argv + 2);
   const bool gpu = argc > 1 && std::string(argv[1]) == "--gpu";
   if (argc < 2 || (!gpu && std::string(argv[1]) != "--checks")) {
     std::printf("usage: test_host --checks | --gpu\n");
