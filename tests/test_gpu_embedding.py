@@ -113,3 +113,20 @@ def test_table_at_an_odd_address_is_refused(hip):
     out = torch.empty((1, 32), dtype=torch.float32, device=DEV)
     with pytest.raises(_lib.HipError, match="2-byte aligned"):
         hip.embedding(d.Q8_0Table(flat[1:].view(4, 34), 32), dev_i32(np.zeros(1, np.int32)), out)
+
+
+def test_outputs_past_two_to_the_31_values(hip):
+    # 525,313 ids of 4096 values: the output's last rows lie past 2^31 values
+    # (4.3 GB of BF16), so its offsets need 64 bits; sampled rows checked
+    vocab, cols = 1000, 4096
+    count = (1 << 31) // cols + 1025
+    rng = np.random.default_rng(77)
+    table = o.q8_0_table(vocab, cols, rng)
+    ids = rng.integers(0, vocab, count).astype(np.int32)
+    step(f"Q8_0 gather of {count} ids x {cols} to BF16 (past 2^31 output values)")
+    out = torch.empty((count, cols), dtype=torch.bfloat16, device=DEV)
+    hip.embedding(table_on_device(table, cols), dev_i32(ids), out)
+    rows = np.array([0, 1, count // 2, (1 << 31) // cols - 1, (1 << 31) // cols, count - 2, count - 1])
+    got = host_bits(out[torch.from_numpy(rows).to(DEV)])
+    del out
+    assert_bits(o.embedding_q8_0_bf16(table, vocab, cols, ids[rows]), got, what="rows past 2^31 values")
