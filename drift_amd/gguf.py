@@ -17,6 +17,7 @@ bytes (tensor/RocmFp4.scala:64-73).
 
 from __future__ import annotations
 
+import math
 import mmap
 import struct
 import warnings
@@ -44,7 +45,10 @@ class GgmlType:
     def byteSize(self, elements: int) -> int:
         if elements % self.values:
             raise FormatError(f"{elements} elements are not whole {self.name} blocks of {self.values}")
-        return elements // self.values * self.bytes
+        size = elements // self.values * self.bytes
+        if size > _INT64_MAX:
+            raise FormatError(f"{elements} {self.name} elements do not fit 2^63 bytes")
+        return size
 
 
 # DType.all's GGUF types (tensor/DType.scala:168-193 and the quant objects).
@@ -62,6 +66,7 @@ UNSUPPORTED_NAMES = {9: "Q8_1", 15: "Q8_K", 16: "IQ2_XXS", 17: "IQ2_XS", 18: "IQ
                      22: "IQ2_S", 25: "I16", 28: "F64", 29: "IQ1_M", 34: "TQ1_0", 35: "TQ2_0", 39: "MXFP4"}
 
 DEFAULT_ALIGNMENT = 32
+_INT64_MAX = (1 << 63) - 1
 _ROCM_SAMPLED_BLOCKS = 4096  # RocmFp4.scala:41-42
 
 
@@ -85,7 +90,12 @@ class StoredTensor:
 
     @property
     def byteSize(self) -> int:
-        return self.dtype.byteSize(int(np.prod(self.shape, dtype=np.int64)) if self.shape else 1)
+        # exact integers: the dimensions of a crafted file can multiply past
+        # an int64, which is refused
+        elements = math.prod(int(d) for d in self.shape)
+        if elements > _INT64_MAX:
+            raise FormatError(f"{self.name} of {list(self.shape)} has more than 2^63 elements")
+        return self.dtype.byteSize(elements)
 
 
 class GgufFile:
@@ -268,7 +278,12 @@ class _Reader:
             if rank > 8:
                 self.fail(f"{name} has {rank} dimensions")
             dims = [self.count(f"{name} dimension") for _ in range(rank)]
-            infos.append((name, dims, self.take("<I"), self.take("<q")))
+            type_id, offset = self.take("<I"), self.take("<q")
+            # an offset before the data section would place the tensor over
+            # the header (the reference's bounds-checked slice refuses it)
+            if offset < 0:
+                self.fail(f"{name} starts {-offset} bytes before the data section")
+            infos.append((name, dims, type_id, offset))
         data_start = (self.position + alignment - 1) // alignment * alignment
         data_bytes = self.size - data_start
         if data_bytes < 0:
@@ -284,7 +299,11 @@ class _Reader:
             if offset % alignment != 0:
                 self.fail(f"{name} is not aligned to {alignment}")
             tensor = StoredTensor(name, t, tuple(reversed(dims)), data_start + offset)
-            if offset + tensor.byteSize > data_bytes:
+            try:
+                size = tensor.byteSize
+            except FormatError as e:
+                self.fail(str(e))
+            if offset + size > data_bytes:
                 self.fail(f"{name} runs past the end of the file")
             described[name] = (tensor, None)
         self.check_spans(infos, described, data_bytes, alignment)

@@ -63,7 +63,10 @@ std::string show(const Value& v) {
 int64_t GgmlType::byteSize(int64_t elements) const {
   if (elements % values != 0)
     throw FormatError(text(elements, " elements are not whole ", name, " blocks of ", values));
-  return elements / values * bytes;
+  int64_t size = 0;
+  if (__builtin_mul_overflow(elements / values, (int64_t)bytes, &size))
+    throw FormatError(text(elements, " ", name, " elements do not fit 2^63 bytes"));
+  return size;
 }
 
 const GgmlType* typeOf(int id, std::string& reason) {
@@ -75,11 +78,17 @@ const GgmlType* typeOf(int id, std::string& reason) {
   return nullptr;
 }
 
-int64_t StoredTensor::byteSize() const {
+// The element count of a shape, refused where it does not fit an int64 (the
+// dimensions of a crafted file can multiply past it).
+static int64_t elementCount(const std::string& name, const std::vector<int64_t>& shape) {
   int64_t elements = 1;
-  for (int64_t d : shape) elements *= d;
-  return type->byteSize(elements);
+  for (int64_t d : shape)
+    if (__builtin_mul_overflow(elements, d, &elements))
+      throw FormatError(text(name, " of ", list(shape), " has more than 2^63 elements"));
+  return elements;
 }
+
+int64_t StoredTensor::byteSize() const { return type->byteSize(elementCount(name, shape)); }
 
 // ---------------------------------------------------------------- reading
 
@@ -188,6 +197,9 @@ class Reader {
       for (uint32_t d = 0; d < rank; ++d) info.dims.push_back(count(info.name + " dimension"));
       info.type = take<uint32_t>();
       info.offset = take<int64_t>();
+      // an offset before the data section would place the tensor over the
+      // header (the reference's bounds-checked slice refuses it when read)
+      if (info.offset < 0) fail(text(info.name, " starts ", -info.offset, " bytes before the data section"));
       infos.push_back(std::move(info));
     }
     const int64_t alignment = f.alignment_;
@@ -207,7 +219,13 @@ class Reader {
       if (info.offset % alignment != 0) fail(text(info.name, " is not aligned to ", alignment));
       StoredTensor tensor{info.name, t, std::vector<int64_t>(info.dims.rbegin(), info.dims.rend()),
                           data_start + info.offset};
-      if (info.offset + tensor.byteSize() > data_bytes) fail(info.name + " runs past the end of the file");
+      int64_t size = 0;
+      try {
+        size = tensor.byteSize();
+      } catch (const FormatError& e) {
+        fail(e.what());
+      }
+      if (info.offset > data_bytes || size > data_bytes - info.offset) fail(info.name + " runs past the end of the file");
       described[info.name] = tensor;
     }
     // Gguf.checkSpans (Gguf.scala:262-285): each tensor's byte size and the

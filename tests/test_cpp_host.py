@@ -13,7 +13,7 @@ import pytest
 
 from drift_amd import gguf
 from oracle import oracle as o
-from tests.test_gguf import header, model_file, one_tensor
+from tests.test_gguf import crafted_files, header, model_file, one_tensor
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 PROGRAM = os.path.join(ROOT, "tests", "cpp", "test_host")
@@ -87,7 +87,7 @@ def test_the_gguf_readers_agree(tmp_path):
              one_tensor(8, [64, 3], 0, q8), one_tensor(2, [64, 2], 0, q8),
              header(tensors=1) + struct.pack("<Q", 1) + b"t" + struct.pack("<I", 9),
              one_tensor(9, [32, 1], 0, bytes(36)), one_tensor(100, [64, 1], 0, rocm.tobytes()),
-             one_tensor(100, [64, 1], 0, bad_rocm.tobytes())]
+             one_tensor(100, [64, 1], 0, bad_rocm.tobytes())] + [blob for blob, _ in crafted_files()]
     for i, blob in enumerate(blobs):
         path = tmp_path / f"case{i}.gguf"
         path.write_bytes(blob)
@@ -96,7 +96,7 @@ def test_the_gguf_readers_agree(tmp_path):
     assert result.returncode == 0, result.stderr
     want = [line for path in files for line in python_summary(path)]
     assert result.stdout.splitlines() == want
-    assert sum(line.startswith("refused ") for line in want) == 13
+    assert sum(line.startswith("refused ") for line in want) == 17
 
 
 def fnv1a(data: bytes) -> int:

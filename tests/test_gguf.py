@@ -96,6 +96,30 @@ def test_refusals_of_the_tensors():
         gguf.read(header(tensors=1) + struct.pack("<Q", 1) + b"t" + struct.pack("<I", 9), "x")
 
 
+def crafted_files():
+    """Files whose tensor records point outside the data or overflow: a
+    negative offset (over the header) and dimensions whose product passes
+    2^63, each with the message both readers give."""
+    q8 = o.quant_table("Q8_0", 2, 64, np.random.default_rng(1)).tobytes()
+    rocm = o.quant_table("Q4_0_ROCMFP4", 1, 64, np.random.default_rng(2)).tobytes()
+    big = [64] + [1 << 10] * 6 + [1 << 4]  # 2^6 * 2^60 * 2^4 = 2^70 values, each dimension within the file's size
+    return [
+        (one_tensor(8, [64, 2], -6528, q8), "t starts 6528 bytes before the data section"),
+        (one_tensor(100, [64, 1], -32, rocm), "t starts 32 bytes before the data section"),
+        (one_tensor(8, big, 0, q8 + bytes(1 << 16)), r"t of \[16, 1024, 1024, 1024, 1024, 1024, 1024, 64\] has "
+                                                    r"more than 2\^63 elements"),
+        # 2^61 F32 values fit an int64, their 2^63 bytes do not
+        (one_tensor(0, [1 << 16, 1 << 16, 1 << 16, 1 << 13], 0, bytes(1 << 17)),
+         r"2305843009213693952 F32 elements do not fit 2\^63 bytes"),
+    ]
+
+
+def test_refusals_of_crafted_offsets_and_sizes():
+    for blob, message in crafted_files():
+        with pytest.raises(gguf.FormatError, match=message):
+            gguf.read(blob, "x")
+
+
 def test_unsupported_types_fail_only_when_asked_for():
     f = gguf.read(one_tensor(9, [32, 1], 0, bytes(36)), "x")  # Q8_1
     assert "t" not in f.tensors and f.unsupported["t"] == "GGML type Q8_1 is not supported yet"
