@@ -415,6 +415,21 @@ void HipOps::addRmsNorm(const Tensor& x, const Tensor& y, const RowNorm& norm, c
   wroteQuantized(target);
 }
 
+void HipOps::groupRmsNorm(const Tensor& x, const Tensor& weight, int groups, float epsilon, float weightOffset,
+                          const Tensor& out) {
+  const int64_t rows = checkRowWise("groupRmsNorm", x, out, {&weight});
+  require(groups > 0 && x.shape.last() % groups == 0, text(x.shape.str(), " in ", groups, " groups"));
+  const int32_t width = (int32_t)(x.shape.last() / groups);
+  if (isBf16(x))
+    launched("drift_rms_norm_bf16", drift_rms_norm_bf16(at<uint16_t>(x), nullptr, at<float>(weight), at<uint16_t>(out),
+                                                         rows * groups, width, epsilon, weightOffset, groups, nullptr,
+                                                         nullptr, nullptr, stream_));
+  else
+    launched("drift_rms_norm_f32", drift_rms_norm_f32(at<float>(x), nullptr, at<float>(weight), at<float>(out),
+                                                       rows * groups, width, epsilon, weightOffset, groups, nullptr,
+                                                       nullptr, nullptr, stream_));
+}
+
 void HipOps::layerNorm(const Tensor& x, const Tensor* weight, const Tensor* bias, float epsilon, const Tensor& out) {
   int64_t rows;
   if (weight && bias)

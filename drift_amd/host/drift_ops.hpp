@@ -232,6 +232,11 @@ class HipOps {
   void rmsNorm(const Tensor& x, const Tensor& weight, float epsilon, float weightOffset, const Tensor& out,
                const QuantizedOutput* quantized = nullptr);
   void addRmsNorm(const Tensor& x, const Tensor& y, const RowNorm& norm, const QuantizedOutput* quantized = nullptr);
+  // RMS norm of each of a row's `groups` equal parts on its own, `weight`
+  // spanning the whole row ([groups × width]); no int8 side output
+  // (ops/NormalisationOps.scala:46-58, ops/HipNormalisation.scala:133-158)
+  void groupRmsNorm(const Tensor& x, const Tensor& weight, int groups, float epsilon, float weightOffset,
+                    const Tensor& out);
   void layerNorm(const Tensor& x, const Tensor* weight, const Tensor* bias, float epsilon, const Tensor& out);
   void modulate(const Tensor& x, const Tensor& scale, const Tensor& shift, const Tensor& out);
   // AdaLN in one launch: layerNorm without affine, then sample s's row of

@@ -261,8 +261,14 @@ def _name(dtype) -> str:
             torch.float8_e4m3fn: "F8_E4M3"}.get(dtype, str(dtype))
 
 
+def _dims(shape) -> str:
+    """A shape as the reference's Shape.toString writes it
+    (tensor/Tensor.scala:12)."""
+    return "[" + "×".join(str(d) for d in shape) + "]"
+
+
 def _shape(t) -> str:
-    return "[" + ", ".join(str(d) for d in t.shape) + "]"
+    return _dims(t.shape)
 
 
 def requireF32(operation: str, *tensors) -> None:
@@ -331,7 +337,7 @@ def checkRope(x, positions, rope: Rope, out) -> tuple:
     count = rope.sections.positionsPerToken
     expected = (tokens,) if count == 1 else (count, tokens)
     _require(tuple(positions.shape) == expected,
-             f"rope positions {_shape(positions)}, expected [{', '.join(map(str, expected))}]")
+             f"rope positions {_shape(positions)}, expected {_dims(expected)}")
     _require(rope.rotaryDimensions % 2 == 0 and rope.rotaryDimensions <= dimension,
              f"rope: {rope.rotaryDimensions} rotary dimensions in heads of {dimension}")
     return tokens, heads, dimension
@@ -569,6 +575,18 @@ class HipOps:
         rows = checkRowWise("addRmsNorm", x, norm.out, norm.weight)
         _on_device("addRmsNorm", x, y, norm.weight, norm.out)
         self._normRows(x, y, norm.weight, norm.epsilon, norm.weightOffset, norm.out, rows)
+
+    def groupRmsNorm(self, x, weight, groups: int, epsilon: float, weightOffset: float, out) -> None:
+        """RMS norm of each of a row's `groups` equal parts on its own, with
+        `weight` spanning the whole row ([groups × width])
+        (ops/NormalisationOps.scala:46-58): rms_norm over rows × groups rows
+        of width values, row r weighted by weight row r % groups, with no
+        int8 side output (ops/HipNormalisation.scala:133-158)."""
+        rows = checkRowWise("groupRmsNorm", x, out, weight)
+        _require(groups > 0 and x.shape[-1] % groups == 0, f"{_shape(x)} in {groups} groups")
+        _on_device("groupRmsNorm", x, weight, out)
+        self._launch(f"drift_rms_norm_{_suffix(x.dtype)}", _ptr(x), None, _ptr(weight), _ptr(out), rows * groups,
+                     x.shape[-1] // groups, epsilon, weightOffset, groups, None, None, None)
 
     def layerNorm(self, x, weight: Optional[torch.Tensor], bias: Optional[torch.Tensor], epsilon: float,
                   out) -> None:
@@ -857,12 +875,12 @@ class HipOps:
         a RotatedTable to BF16 (ops/HipBase.scala:276-311)."""
         if isinstance(table, RotatedTable):
             _require(out.dtype == BF16, f"convert: no conversion from {table.dtype} to {_name(out.dtype)}")
-            _require(tuple(out.shape) == table.shape, f"convert: out {_shape(out)} for {list(table.shape)}")
+            _require(tuple(out.shape) == table.shape, f"convert: out {_shape(out)} for {_dims(table.shape)}")
             self._rotated("drift_rotated_dequantize_bf16", table, out)
             return
         t = self._checkStored("dequantize", table)
         _require(out.dtype in (BF16, F16), f"dequantize writes BF16 or F16, not {_name(out.dtype)}")
-        _require(tuple(out.shape) == table.shape, f"dequantize: out {_shape(out)} for a table {list(table.shape)}")
+        _require(tuple(out.shape) == table.shape, f"dequantize: out {_shape(out)} for a table {_dims(table.shape)}")
         _require(table.cols % 8 == 0 or t.values == 1,
                  f"dequantize: rows of {table.cols} values (quant kernels take multiples of 8)")
         _on_device("dequantize", table.data, out)

@@ -85,6 +85,8 @@ CHECK_TEST(row_wise_checks_carry_the_reference_messages) {
   refused([&] { hip.rmsNorm(x, w, 1e-6f, 0.0f, fake(DType::BF16, {3, 7})); },
           "rmsNorm takes one type, not F32 and BF16");
   refused([&] { hip.rmsNorm(x, fake(DType::BF16, {7}), 1e-6f, 0.0f, x); }, "rmsNorm takes F32, not BF16");
+  refused([&] { hip.groupRmsNorm(x, w, 2, 1e-6f, 0.0f, x); }, "requirement failed: [3×7] in 2 groups");
+  refused([&] { hip.groupRmsNorm(x, fake(DType::F32, {6}), 7, 1e-6f, 0.0f, x); }, "groupRmsNorm: [6] for rows of 7");
   refused([&] { hip.layerNorm(fake(DType::BF16, {3, 7}), nullptr, nullptr, 1e-6f, fake(DType::BF16, {3, 7})); },
           "layerNorm takes F32, not BF16");
   refused([&] { hip.addRmsNorm(x, fake(DType::F32, {3, 6}), RowNorm{w, 1e-6f, 0.0f, x}); },
@@ -310,6 +312,21 @@ GPU_TEST(rms_norm_f32_and_bf16) {
   std::vector<float> xf = from_bf16(xb), wantf(xf.size());
   oracle_rms_norm(xf.data(), nullptr, w2.data(), wantf.data(), r2, c2, 1e-5f, 0.0f, 1);
   within_ulp(to_bf16(wantf), dev.download<uint16_t>(outb), "rmsNorm bf16");
+}
+
+// groupRmsNorm: each of a row's groups normed on its own with its slice of
+// the weights (ops/HipNormalisation.scala:133-158)
+GPU_TEST(group_rms_norm) {
+  HipOps hip;
+  Device dev;
+  const int64_t rows = 6, groups = 3, width = 1024, cols = groups * width;
+  std::vector<float> x = gaussian(21, rows * cols, 2.0f), w = gaussian(22, cols);
+  const Tensor xd = dev.upload(DType::F32, {rows, cols}, x), wd = dev.upload(DType::F32, {cols}, w);
+  const Tensor out = dev.empty(DType::F32, {rows, cols});
+  hip.groupRmsNorm(xd, wd, (int)groups, 1e-6f, 0.5f, out);
+  std::vector<float> want(x.size());
+  oracle_rms_norm(x.data(), nullptr, w.data(), want.data(), rows * groups, width, 1e-6f, 0.5f, (int)groups);
+  close_f32(want, dev.download<float>(out), "groupRmsNorm f32");
 }
 
 GPU_TEST(adaln_bf16_two_samples) {

@@ -120,6 +120,66 @@ def test_rms_norm_does_not_depend_on_the_batch(hip, dtype, cols):
     assert np.array_equal(host(few).view(np.uint8), host(batch)[100:107].view(np.uint8)), "rows 100-106"
 
 
+# (rows, groups, width) of the group norm, one case for each way the library
+# splits a row: a thread per narrow row (<= 32 values), the scalar path
+# (widths not whole 16-byte chunks), a wave or a 4-wave group per row in a
+# batch, and the 8- or 16-wave group a few long rows take
+GROUP_SHAPES = [(300, 2, 16), (41, 3, 3), (9, 3, 37), (64, 4, 512), (33, 2, 4096), (1, 2, 4096), (2, 3, 8192),
+                (3, 4, 2560)]
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("rows,groups,width", GROUP_SHAPES)
+def test_group_rms_norm(hip, dtype, rows, groups, width):
+    # groupRmsNorm (ops/HipNormalisation.scala:133-158): rms_norm over rows x
+    # groups rows of `width`, row r weighted by weight row r % groups
+    step(f"groupRmsNorm {dtype} [{rows}, {groups} x {width}]")
+    x = gaussian(41, (rows, groups * width), 2.0)
+    w = (1 + 0.1 * gaussian(42, groups * width)).astype(np.float32)
+    want_rows = (rows * groups, width)
+    if dtype == "f32":
+        out = torch.empty((rows, groups * width), dtype=torch.float32, device=DEV)
+        hip.groupRmsNorm(dev_f32(x), dev_f32(w), groups, 1e-6, 0.25, out)
+        want = o.rms_norm(x.reshape(want_rows), w.reshape(groups, width), 1e-6, 0.25, weight_rows=groups)
+        assert_f32(want.reshape(rows, -1), host_f32(out), what="groupRmsNorm")
+    else:
+        xb = bf16_input(x)
+        out = torch.empty((rows, groups * width), dtype=torch.bfloat16, device=DEV)
+        hip.groupRmsNorm(dev_bf16(xb), dev_f32(w), groups, 1e-5, 0.0, out)
+        want = o.rms_norm_bf16(xb.reshape(want_rows), w.reshape(groups, width), 1e-5, weight_rows=groups)
+        assert_bf16(want.reshape(rows, -1), host_bits(out), what="groupRmsNorm bf16")
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("rows,groups,width", GROUP_SHAPES)
+def test_weight_rows_with_a_residual(hip, dtype, rows, groups, width):
+    # rms_norm's weight_rows with y through the C ABI: x += y written back,
+    # then row r of the sum normed with weight row r % weight_rows
+    step(f"rms_norm {dtype} weight_rows {groups} with y, [{rows * groups}, {width}]")
+    shape = (rows * groups, width)
+    x, y = gaussian(43, shape), gaussian(44, shape)
+    w = gaussian(45, (groups, width))
+    entry = f"drift_rms_norm_{dtype}"
+    wd = dev_f32(w)  # every device tensor held until the launch has run
+    if dtype == "f32":
+        xd, yd = dev_f32(x), dev_f32(y)
+        out = torch.empty(shape, dtype=torch.float32, device=DEV)
+        hip._launch(entry, d._ptr(xd), d._ptr(yd), d._ptr(wd), d._ptr(out), shape[0], width, 1e-6, 0.0, groups,
+                    None, None, None)
+        summed, want = o.rms_norm(x, w, 1e-6, 0.0, y=y, weight_rows=groups)
+        assert np.array_equal(host_f32(xd), summed), "x += y is the F32 sum"
+        assert_f32(want, host_f32(out), what="weight_rows with y")
+    else:
+        xb, yb = bf16_input(x), bf16_input(y)
+        xd, yd = dev_bf16(xb), dev_bf16(yb)
+        out = torch.empty(shape, dtype=torch.bfloat16, device=DEV)
+        hip._launch(entry, d._ptr(xd), d._ptr(yd), d._ptr(wd), d._ptr(out), shape[0], width, 1e-6, 0.0, groups,
+                    None, None, None)
+        summed, want = o.rms_norm_bf16(xb, w, 1e-6, y_bits=yb, weight_rows=groups)
+        assert np.array_equal(host_bits(xd), summed), "x += y rounds the F32 sum to bf16"
+        assert_bf16(want, host_bits(out), what="weight_rows with y, bf16")
+
+
 def test_rms_norm_in_place_and_zero_rows(hip):
     step("rmsNorm in place, zero row")
     x = gaussian(8, (6, 512))

@@ -38,6 +38,11 @@ def test_row_vectors_must_match_rows(hip):
         hip.rmsNorm(bf16(2, 4), f32(4), 1e-6, 0.0, f32(2, 4))
     with pytest.raises(ValueError, match=r"modulate: \[5\] for rows of 4"):
         hip.modulate(f32(2, 4), f32(4), f32(5), f32(2, 4))
+    # groupRmsNorm (ops/HipNormalisation.scala:141-142): weights span the row
+    with pytest.raises(ValueError, match=r"groupRmsNorm: \[2\] for rows of 4"):
+        hip.groupRmsNorm(f32(2, 4), f32(2), 2, 1e-6, 0.0, f32(2, 4))
+    with pytest.raises(ValueError, match=r"^\[2×6\] in 4 groups$"):
+        hip.groupRmsNorm(f32(2, 6), f32(6), 4, 1e-6, 0.0, f32(2, 6))
 
 
 def test_rope_rules(hip):
@@ -46,7 +51,7 @@ def test_rope_rules(hip):
         hip.rope(f32(4, 128), torch.zeros(4, dtype=torch.int32), rope, f32(4, 128))
     with pytest.raises(ValueError, match="positions are I32, not F32"):
         hip.rope(f32(4, 2, 128), f32(4), rope, f32(4, 2, 128))
-    with pytest.raises(ValueError, match=r"positions \[4\], expected \[3, 4\]"):
+    with pytest.raises(ValueError, match=r"positions \[4\], expected \[3×4\]"):
         mrope = d.Rope(1e6, 64, d.RopeLayout.Neox, d.RopeSections.Contiguous(11, 11, 10))
         hip.rope(f32(4, 2, 128), torch.zeros(4, dtype=torch.int32), mrope, f32(4, 2, 128))
     with pytest.raises(ValueError, match="axes of"):
@@ -67,7 +72,7 @@ def test_embedding_rules(hip):
     table = d.Q8_0Table(torch.zeros(10, 68, dtype=torch.uint8), 64)
     with pytest.raises(ValueError, match="ids are I32"):
         hip.embedding(table, torch.zeros(3, dtype=torch.int64), f32(3, 64))
-    with pytest.raises(ValueError, match=r"out \[3, 32\] for 3 rows of 64"):
+    with pytest.raises(ValueError, match=r"out \[3×32\] for 3 rows of 64"):
         hip.embedding(table, torch.zeros(3, dtype=torch.int32), f32(3, 32))
 
 
@@ -89,19 +94,19 @@ def test_gated_residual_rules(hip):
         hip.gatedAdd(f32(2, 4), f32(3, 4), f32(4))
     with pytest.raises(ValueError, match="rowsPerSample"):
         hip.gatedAdd(f32(4, 4), f32(4, 4), f32(2, 4))
-    with pytest.raises(ValueError, match=r"gatedAdd: \[3, 4\] for 2 samples"):
+    with pytest.raises(ValueError, match=r"gatedAdd: \[3×4\] for 2 samples"):
         hip.gatedAdd(f32(4, 4), f32(4, 4), f32(3, 4), rowsPerSample=2)
-    with pytest.raises(ValueError, match=r"modulateChunks takes \[rows, C\], not \[2, 2, 4\]"):
+    with pytest.raises(ValueError, match=r"modulateChunks takes \[rows, C\], not \[2×2×4\]"):
         hip.modulateChunks(f32(2, 2, 4), f32(2, 24), 0, 1, f32(2, 2, 4))
-    with pytest.raises(ValueError, match=r"modulateChunks: table \[2, 10\] for \[2, 4\], chunks ArraySeq\(0, 1\)"):
+    with pytest.raises(ValueError, match=r"modulateChunks: table \[2×10\] for \[2×4\], chunks ArraySeq\(0, 1\)"):
         hip.modulateChunks(f32(2, 4), f32(2, 10), 0, 1, f32(2, 4))
-    with pytest.raises(ValueError, match=r"gatedAddChunk: table \[2, 24\] for \[2, 4\], chunks ArraySeq\(6\)"):
+    with pytest.raises(ValueError, match=r"gatedAddChunk: table \[2×24\] for \[2×4\], chunks ArraySeq\(6\)"):
         hip.gatedAddChunk(f32(2, 4), f32(2, 4), f32(2, 24), 6)
     with pytest.raises(ValueError, match="takes F32, not BF16"):
         hip.gatedAddChunk(f32(2, 4), f32(2, 4), bf16(2, 24), 2)
     with pytest.raises(ValueError, match=r"rowGatedAdd takes \[rows, cols\], not \[8\]"):
         hip.rowGatedAdd(f32(8), f32(8), f32(1))
-    with pytest.raises(ValueError, match=r"rowGatedAdd: gate \[3\] for \[2, 4\]"):
+    with pytest.raises(ValueError, match=r"rowGatedAdd: gate \[3\] for \[2×4\]"):
         hip.rowGatedAdd(f32(2, 4), f32(2, 4), f32(3))
     # a call that passes the rules stops at the device check
     with pytest.raises(ValueError, match="device memory"):
@@ -124,7 +129,7 @@ def test_the_cache_and_its_writes_are_checked(hip):
         d.KvCache(f32(4, 16, 2, 8), f16(4, 2, 8, 16), 16)
     cache = d.KvCache(f16(4, 16, 2, 8), f16(4, 2, 8, 16), 16)
     # ops/AttentionOps.scala:225-256
-    with pytest.raises(ValueError, match=r"cacheWrite: \[3, 3, 8\] into a cache of 2 heads of 8"):
+    with pytest.raises(ValueError, match=r"cacheWrite: \[3×3×8\] into a cache of 2 heads of 8"):
         hip.cacheWrite(f32(3, 3, 8), f32(3, 3, 8), cache, i32(4), 0)
     with pytest.raises(ValueError, match="a page table of 1 pages for 19 positions"):
         hip.cacheWrite(f32(3, 2, 8), f32(3, 2, 8), cache, i32(1), 16)
@@ -137,7 +142,7 @@ def test_the_cache_and_its_writes_are_checked(hip):
 
 
 def test_split_halves_and_attention_inputs_are_checked(hip):
-    with pytest.raises(ValueError, match=r"splitHalves: \[2, 10\] into \[2, 4\]"):
+    with pytest.raises(ValueError, match=r"splitHalves: \[2×10\] into \[2×4\]"):
         hip.splitHalves(f32(2, 10), f32(2, 4), f32(2, 4))
     cache = d.KvCache(f16(4, 16, 2, 8), f16(4, 2, 8, 16), 16)
     norms = d.QueryKeyNorms(f32(8), f32(8), 1e-6, 0.0, d.Rope(1e4, 8))
@@ -161,7 +166,7 @@ def test_rotated_weights_are_checked_as_checkRotated_does(hip):
     t = hip.rotated(codes, d.ConvRotParts(scales))
     assert t.shape == (4, 256) and t.dtype == "CONVROT_I8"
     assert hip.rotated(codes, d.ConvRotParts(torch.ones(1))).shape == (4, 256)
-    with pytest.raises(ValueError, match=r"rotated: U8 codes \[4, 256\]"):
+    with pytest.raises(ValueError, match=r"rotated: U8 codes \[4×256\]"):
         hip.rotated(codes.view(torch.uint8), d.ConvRotParts(scales))
     with pytest.raises(ValueError, match="rotated: rows of 200 columns"):
         hip.rotated(torch.zeros((4, 200), dtype=torch.int8), d.ConvRotParts(scales))
@@ -178,10 +183,10 @@ def test_rotated_weights_are_checked_as_checkRotated_does(hip):
     with pytest.raises(ValueError, match=r"rotated: a codebook F32 \[8\]"):
         hip.rotated(torch.zeros((4, 256), dtype=torch.int8), d.ConvRotParts(scales, d.ConvRotLevels(
             torch.zeros(8), torch.zeros((4, 16), dtype=torch.uint8), 32)))
-    with pytest.raises(ValueError, match=r"rotated: relative scales U8 \[4, 8\]"):
+    with pytest.raises(ValueError, match=r"rotated: relative scales U8 \[4×8\]"):
         hip.rotated(torch.zeros((4, 256), dtype=torch.int8), d.ConvRotParts(scales, d.ConvRotLevels(
             torch.zeros(16), torch.zeros((4, 8), dtype=torch.uint8), 32)))
-    with pytest.raises(ValueError, match="embedding: out \\[3, 256\\] for 2 rows of 256"):
+    with pytest.raises(ValueError, match="embedding: out \\[3×256\\] for 2 rows of 256"):
         hip.embedding(t, torch.zeros(2, dtype=torch.int32), torch.empty((3, 256)))
     with pytest.raises(ValueError, match="convert: no conversion from CONVROT_I8 to F32"):
         hip.convert(t, torch.empty((4, 256)))
