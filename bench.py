@@ -17,19 +17,24 @@ Inputs are synthetic (seeded device generators) and resident in HBM. Each
 kernel rotates through buffer sets totalling more than 512 MB, so the 256 MB
 Infinity Cache cannot hold what the next launch reads.
 
-The timed region runs K steps' launches grouped by kernel (K launches of one
-kernel, then K of the next), so no kernel reads what the kernel before it
-left in the Infinity Cache or pays for the dirty lines it left there. Every
-call is checked by the Ops layer beforehand; the timed loop makes the C-ABI
-calls those checks produced, with their HIP events created in advance, so
-the host stays ahead of the GPU.
+The timed region replays, kernel by kernel, a HIP graph holding that
+kernel's K launches (K launches of one kernel, then K of the next), so no
+kernel reads what the kernel before it left in the Infinity Cache or pays
+for the dirty lines it left there, and no host call sits between launches.
+Every call is checked by the Ops layer beforehand; the graphs capture the
+C-ABI calls those checks produced. The same launches made one by one from
+Python are timed too (`us_eager`), and `host_us_per_call` is the C++ host
+cost of one call of each entry point (drift_amd/host/launch_cost).
 
 Printed: one JSON line. `value` is the step's algorithmic bytes (the reads
 and writes of the tensors each op names) over the step's wall time;
 `kernels` has each kernel's HIP-event time, GB/s, fraction of the 8 TB/s HBM
-peak and rows/s; `roofline` is the dominant kernel's; `cpu_baseline` is the
-CPU reference arithmetic (the oracle) timed on a bounded sample of the same
-work on this host's cores, scaled to the whole step.
+peak, fraction of its ceiling and rows/s; `ceilings` is the streaming probe
+(drift_stream_mix) moving each long kernel's bytes in its read:write mix,
+and the reference's streaming read (drift_read_sum_f32x4) over 1 GiB;
+`roofline` is the dominant kernel's; `cpu_baseline` is the CPU reference
+arithmetic (the oracle) timed on a bounded sample of the same work on this
+host's cores, scaled to the whole step.
 """
 
 from __future__ import annotations
@@ -42,7 +47,9 @@ import math
 import os
 import sys
 import time
+import subprocess
 from concurrent.futures import ThreadPoolExecutor
+from typing import Optional
 
 import numpy as np
 import torch
@@ -60,50 +67,50 @@ DEV = "cuda:0"
 
 class Kernel:
     """One fused kernel at one configuration: its launch over buffer set i,
-    its algorithmic bytes and rows per launch, and a CPU reference leg."""
+    its algorithmic bytes (and how many of them are reads) and rows per
+    launch, and a CPU reference leg."""
 
-    def __init__(self, name, config, bytes_per_call, rows, launch, sets=1, cpu=None):
+    def __init__(self, name, config, bytes_per_call, rows, launch, sets=1, read_bytes=None):
         self.name, self.config = name, config
         self.sets = sets
         self.calls = []
         self.bytes, self.rows = bytes_per_call, rows
+        self.read_bytes = bytes_per_call // 2 if read_bytes is None else read_bytes
         self.launch = launch
-        self.cpu = cpu  # (sample description, seconds for the sample, fraction of a call the sample is)
+        self.cpu = None  # (sample description, seconds for the sample, fraction of a call the sample is)
         self.cpu_all = None  # (threads, seconds for the same sample split across them)
-        self.times_ms = []
+        self.graph_ms = None  # average launch, replayed from a captured graph
+        self.eager_ms = None  # average launch, each made from Python through ctypes
+        self.ceiling = None  # the stream probe at this kernel's bytes and read/write mix
 
     def prepare(self, ops: "Prepared") -> None:
         """Runs the Ops checks of every buffer set's call and keeps the C-ABI
-        calls they produce (none for a launch that is not an Ops call)."""
+        call each produces."""
         lib = _lib.load()
         for i in range(self.sets):
             ops.kept = None
             self.launch(i)
             if ops.kept is None:
-                self.calls = []
-                return
+                raise RuntimeError(f"{self.name}: the launch made no C-ABI call")
             entry, args = ops.kept
             self.calls.append((entry, getattr(lib, entry), args))
 
-    def fire(self, i: int) -> None:
-        if not self.calls:
-            self.launch(i)
-            return
+    def fire(self, i: int, stream) -> None:
         entry, fn, args = self.calls[i % len(self.calls)]
-        code = fn(*args)
+        code = fn(*args, stream)
         if code != 0:
             raise _lib.HipError(entry, code, _lib.load().drift_last_error().decode())
 
 
 class Prepared(d.HipOps):
     """The Ops layer with its checks, keeping the call each method would make
-    instead of making it."""
+    (without its stream) instead of making it."""
 
     kept = None
 
     def _launch(self, entry: str, *args) -> None:
         self.onWork()
-        self.kept = (entry, args + (self._stream(),))
+        self.kept = (entry, args)
 
 
 def sets_for(bytes_per_call: int, floor: int = 2, cap: int = 64) -> int:
@@ -151,7 +158,8 @@ def make_kernels(hip: d.HipOps):
         w = (1 + 0.1 * torch.randn(4096, generator=gen(1), device=DEV)).float()
         kernels.append(Kernel(f"rms_norm_bf16_b{b}", f"C2 RMSNorm bf16 [{b},4096] eps 1e-5", nbytes, b,
                               lambda i, xs=xs, outs=outs, w=w: hip.rmsNorm(xs[i % len(xs)], w, 1e-5, 0.0,
-                                                                           outs[i % len(outs)]), sets=n))
+                                                                           outs[i % len(outs)]), sets=n,
+                              read_bytes=b * 4096 * 2 + 4096 * 4))
         nbytes = 3 * b * 14336 * 2
         n = sets_for(nbytes, 8, 8)
         gs = [randn_bf16((b, 14336), 100 + i) for i in range(n)]
@@ -160,7 +168,7 @@ def make_kernels(hip: d.HipOps):
         kernels.append(Kernel(f"swiglu_bf16_b{b}", f"C2 SwiGLU bf16 [{b},14336]", nbytes, b,
                               lambda i, gs=gs, us=us, os_=os_: hip.gated(d.Activation.Silu, gs[i % len(gs)],
                                                                          us[i % len(us)], os_[i % len(os_)]),
-                              sets=n))
+                              sets=n, read_bytes=2 * b * 14336 * 2))
 
     # The int8 side output for the decode products: F32 RMSNorm [B, 4096] and
     # SwiGLU [B, 14336] writing their output quantized too (codes 1 B per
@@ -175,7 +183,8 @@ def make_kernels(hip: d.HipOps):
         kernels.append(Kernel(f"rms_norm_q8_f32_b{b}", f"RMSNorm f32 [{b},4096] + int8 side output", nbytes, b,
                               lambda i, xs=xs, outs=outs, sides=sides, w=w, b=b: hip._launch(
                                   "drift_rms_norm_f32", *side_args(xs[i % len(xs)], None, w, outs[i % len(outs)], b,
-                                                                   4096, sides[i % len(sides)])), sets=n))
+                                                                   4096, sides[i % len(sides)])), sets=n,
+                              read_bytes=b * 4096 * 4 + 4096 * 4))
         n = sets_for(b * 14336 * 13, 8, 8)
         gs = [(0.5 * torch.randn((b, 14336), generator=gen(900 + i), device=DEV)) for i in range(n)]
         us = [(0.5 * torch.randn((b, 14336), generator=gen(950 + i), device=DEV)) for i in range(n)]
@@ -186,7 +195,8 @@ def make_kernels(hip: d.HipOps):
                               lambda i, gs=gs, us=us, os_=os_, sides=sides, b=b: hip._launch(
                                   "drift_gated_f32", *gated_side_args(gs[i % len(gs)], us[i % len(us)],
                                                                       os_[i % len(os_)], b * 14336,
-                                                                      sides[i % len(sides)])), sets=n))
+                                                                      sides[i % len(sides)])), sets=n,
+                              read_bytes=2 * b * 14336 * 4))
 
     # C3 prefill: per-head RMSNorm (eps 1e-6) + NeoX RoPE (theta 1e6)
     t, hq, hk, dim = 4096, 32, 8, 128
@@ -203,7 +213,8 @@ def make_kernels(hip: d.HipOps):
     kernels.append(Kernel("qk_norm_rope_bf16", "C3 per-head RMSNorm + NeoX RoPE bf16 Q[4096,32,128] K[4096,8,128]",
                           nbytes, t,
                           lambda i, n=n: hip.queryKeyNormRope(qs[i % n], ks[i % n], norms, positions, rqs[i % n],
-                                                              rks[i % n]), sets=n))
+                                                              rks[i % n]), sets=n,
+                          read_bytes=t * (hq + hk) * dim * 2 + t * 4 + 2 * dim * 4))
 
     # The same prefill through the dense decoders' whole attention-input step:
     # per-head norms, NeoX rope, and keys and values into the paged F16 cache
@@ -217,7 +228,7 @@ def make_kernels(hip: d.HipOps):
                           "K[4096,8,128] bf16, K and V[4096,8,128] into a paged F16 cache", nbytes_ai, t,
                           lambda i, n=n: hip.queryKeyNormRopeCache(qs[i % n], ks[i % n], vs[i % n], norms, positions,
                                                                    caches[i % n], tables[i % n], 0, rqs[i % n]),
-                          sets=n))
+                          sets=n, read_bytes=t * (hq + 2 * hk) * dim * 2 + t * 4 + 2 * dim * 4 + pages * 4))
 
     # C4: Q8_0 gather, 8192 ids from [151936, 4096] to bf16
     vocab, cols, count = 151936, 4096, 8192
@@ -237,7 +248,8 @@ def make_kernels(hip: d.HipOps):
             for i in range(n)]
     gouts = [torch.empty((count, cols), dtype=torch.bfloat16, device=DEV) for _ in range(n)]
     kernels.append(Kernel("embedding_q8_0_bf16", "C4 Q8_0 gather 8192 ids from [151936,4096] to bf16", nbytes,
-                          count, lambda i, n=n: hip.embedding(q8, idss[i % n], gouts[i % n]), sets=n))
+                          count, lambda i, n=n: hip.embedding(q8, idss[i % n], gouts[i % n]), sets=n,
+                          read_bytes=count * blocks * 34 + count * 4))
 
     # C5: Video DiT block, x [2 * 32760, 3072]
     rows, width, per = 2 * 32760, 3072, 32760
@@ -249,16 +261,17 @@ def make_kernels(hip: d.HipOps):
     nbytes = 2 * rows * width * 2 + 2 * 2 * width * 4
     kernels.append(Kernel("adaln_bf16", "C5 AdaLN LN(eps 1e-6)*(1+scale)+shift bf16 [65520,3072]", nbytes, rows,
                           lambda i, n=n: hip.layerNormModulate(xs5[i % n], scale, shift, 1e-6, outs5[i % n], per),
-                          sets=n))
+                          sets=n, read_bytes=rows * width * 2 + 2 * 2 * width * 4))
     nbytes = 2 * rows * width * 2
     kernels.append(Kernel("gelu_tanh_bf16", "C5 GELU-tanh bf16 in place [65520,3072]", nbytes, rows,
                           lambda i, n=n: hip.activation(d.Activation.GeluTanh, outs5[i % n], outs5[i % n]),
-                          sets=n))
+                          sets=n, read_bytes=rows * width * 2))
     qs5 = [randn_bf16((rows, 24, 128), 700 + i) for i in range(n)]
     rq5 = [torch.empty_like(qs5[0]) for _ in range(n)]
     nbytes = 2 * rows * 24 * 128 * 2
     kernels.append(Kernel("rope_3d_bf16", "C5 3-D RoPE bf16 Q[65520,24,128] grid 21x30x52 theta 1e4", nbytes, rows,
-                          lambda i, n=n: hip.rope3d(qs5[i % n], 21, 30, 52, rq5[i % n]), sets=n))
+                          lambda i, n=n: hip.rope3d(qs5[i % n], 21, 30, 52, rq5[i % n]), sets=n,
+                          read_bytes=rows * 24 * 128 * 2))
 
     # The same block's gated residuals and per-row modulation (bf16 x, F32
     # gates and tables): x += gate[sample] * y; out = x * (1 + t[r][4]) +
@@ -268,23 +281,27 @@ def make_kernels(hip: d.HipOps):
     gates = (0.5 * torch.randn((2, width), generator=gen(8), device=DEV)).float()
     nbytes = rows * width * 6 + 2 * width * 4
     kernels.append(Kernel("gated_add_bf16", "C5 gated residual x += gate[sample] * y bf16 [65520,3072]", nbytes, rows,
-                          lambda i, n=n: hip.gatedAdd(xs5[i % n], ys5[i % n], gates, per), sets=n))
+                          lambda i, n=n: hip.gatedAdd(xs5[i % n], ys5[i % n], gates, per), sets=n,
+                          read_bytes=rows * width * 4 + 2 * width * 4))
     table = torch.empty((rows, 6 * width), dtype=torch.float32, device=DEV)
     for lo in range(0, rows, 8192):
         table[lo:lo + 8192] = 0.3 * torch.randn((min(8192, rows - lo), 6 * width), generator=gen(9), device=DEV)
     nbytes = rows * width * (2 + 2 + 4 + 4)
     kernels.append(Kernel("modulate_chunks_bf16", "C5 per-row modulation out = x*(1+t[r][4])+t[r][3] bf16 [65520,3072], "
                           "t F32 [65520,18432]", nbytes, rows,
-                          lambda i, n=n: hip.modulateChunks(xs5[i % n], table, 3, 4, outs5[i % n]), sets=n))
+                          lambda i, n=n: hip.modulateChunks(xs5[i % n], table, 3, 4, outs5[i % n]), sets=n,
+                          read_bytes=rows * width * 10))
     nbytes = rows * width * (2 + 2 + 2 + 4)
     kernels.append(Kernel("gated_add_chunk_bf16", "C5 per-row gated residual x += t[r][5] * y bf16 [65520,3072]",
-                          nbytes, rows, lambda i, n=n: hip.gatedAddChunk(xs5[i % n], ys5[i % n], table, 5), sets=n))
+                          nbytes, rows, lambda i, n=n: hip.gatedAddChunk(xs5[i % n], ys5[i % n], table, 5), sets=n,
+                          read_bytes=rows * width * 8))
     heads = rows * 24
     head_gates = torch.rand(heads, generator=gen(10), device=DEV).float()
     nbytes = heads * 128 * 6 + heads * 4
     kernels.append(Kernel("row_gated_add_bf16", "per-head gate x[r] += g[r] * y[r] bf16 [65520*24,128]", nbytes, heads,
                           lambda i, n=n: hip.rowGatedAdd(qs5[i % n].view(heads, 128), rq5[i % n].view(heads, 128),
-                                                         head_gates), sets=n))
+                                                         head_gates), sets=n,
+                          read_bytes=heads * 128 * 4 + heads * 4))
 
     # Weights decoded for the GEMM path: a Q4_K GGUF weight [14336, 4096] to
     # bf16, and ComfyUI's rotated linears (int8 codes, and 4-bit codes with
@@ -301,7 +318,8 @@ def make_kernels(hip: d.HipOps):
         q4k.append(d.StoredTable(raw.view(rows_k, -1), d.STORAGE_TYPES["Q4_K"], cols_k))
     kouts = [torch.empty((rows_k, cols_k), dtype=torch.bfloat16, device=DEV) for _ in range(n)]
     kernels.append(Kernel("dequantize_q4_k_bf16", "Q4_K weight [14336,4096] decoded to bf16", nbytes, rows_k,
-                          lambda i, n=n: hip.dequantize(q4k[i % n], kouts[i % n]), sets=n))
+                          lambda i, n=n: hip.dequantize(q4k[i % n], kouts[i % n]), sets=n,
+                          read_bytes=rows_k * cols_k // 256 * 144))
     rows_r, cols_r, group = 13824, 5120, 64
     for four in (False, True):
         code_bytes = rows_r * cols_r // (2 if four else 1)
@@ -323,7 +341,8 @@ def make_kernels(hip: d.HipOps):
         name = "rotated_dequantize_w4a8_bf16" if four else "rotated_dequantize_i8_bf16"
         what = "4-bit (fp8 scales a 64 columns)" if four else "int8"
         kernels.append(Kernel(name, f"ConvRot rotated linear, {what} codes [13824,5120] decoded to bf16", nbytes,
-                              rows_r, lambda i, n=n, w=weights, o_=routs: hip.convert(w[i % n], o_[i % n]), sets=n))
+                              rows_r, lambda i, n=n, w=weights, o_=routs: hip.convert(w[i % n], o_[i % n]), sets=n,
+                              read_bytes=nbytes - rows_r * cols_r * 2))
     return kernels
 
 
@@ -362,7 +381,13 @@ def cpu_baseline(kernels, budget_s: float):
     w4096 = (1 + 0.1 * rng.standard_normal(4096)).astype(np.float32)
     w128 = (1 + 0.1 * rng.standard_normal(128)).astype(np.float32)
     sc = (0.1 * rng.standard_normal((1, 3072))).astype(np.float32)
-    table = o.q8_0_table(4096, 4096, rng)
+    # the C4 table at its full size, [151936, 4096] (661 MB), so the gather
+    # reads rows the host caches do not hold, as the GPU's does: codes random
+    # bytes, scales fp16 in [1e-3, 2e-2]
+    vocab = 151936
+    table = np.frombuffer(rng.bytes(vocab * 128 * 34), np.uint8).reshape(vocab * 128, 34).copy()
+    table[:, 0:2] = rng.uniform(1e-3, 2e-2, vocab * 128).astype(np.float16).view(np.uint8).reshape(-1, 2)
+    table = table.reshape(vocab, 128 * 34)
 
     def rms(units):
         x = bits((units, 4096))
@@ -396,8 +421,8 @@ def cpu_baseline(kernels, budget_s: float):
                                                0, gated=False)
 
     def gather(units):
-        ids = rng.integers(0, 4096, units).astype(np.int32)
-        return lambda: o.embedding_q8_0_bf16(table, 4096, 4096, ids)
+        ids = rng.integers(0, vocab, units).astype(np.int32)
+        return lambda: o.embedding_q8_0_bf16(table, vocab, 4096, ids)
 
     def adaln(units):
         x = bits((units, 3072))
@@ -488,7 +513,7 @@ def cpu_baseline(kernels, budget_s: float):
             fn()
             spent += time.perf_counter() - t0
             runs += 1
-        k.cpu = (f"{units} of {total} {unit} x {runs} runs", spent / runs, units / total)
+        k.cpu = (f"{units} of {total} {unit}, {runs} runs", spent / runs, units / total)
         del fn
         t = max(1, min(threads, units))
         parts = [make(units // t + (1 if i < units % t else 0)) for i in range(t)]
@@ -503,6 +528,108 @@ def cpu_baseline(kernels, budget_s: float):
                 spent += time.perf_counter() - t0
                 runs += 1
         k.cpu_all = (t, spent / runs)
+
+
+# ------------------------------------------------------------------ ceilings
+
+def ceiling_probes(k: Kernel, lib) -> list:
+    """The stream probe (drift_stream_mix) moving k's read and write bytes
+    with 1, 2 and 4 chunks a lane, over buffer sets totalling more than
+    512 MB like the kernel's; the fastest is k's ceiling."""
+    reads = -(-k.read_bytes // 16)
+    writes = -(-(k.bytes - k.read_bytes) // 16)
+    n = sets_for(16 * (reads + writes))
+    buffers = [(torch.empty(max(reads, 1) * 16, dtype=torch.uint8, device=DEV).fill_(7),
+                torch.empty(writes * 16, dtype=torch.uint8, device=DEV)) for _ in range(n)]
+    probes = []
+    for per in (1, 2, 4):
+        probe = Kernel(f"ceiling of {k.name}", f"{reads} chunks read, {writes} written, {per} a lane",
+                       16 * (reads + writes), k.rows, None, n, read_bytes=16 * reads)
+        probe.per_lane = per
+        probe.buffers = buffers
+        for src, dst in buffers:
+            probe.calls.append(("drift_stream_mix", lib.drift_stream_mix,
+                                (ctypes.c_void_p(src.data_ptr()), reads, ctypes.c_void_p(dst.data_ptr()), writes, per)))
+        probes.append(probe)
+    return probes
+
+
+def read_probe(lib, gib_bytes: int, blocks: int, name: str) -> Kernel:
+    """The reference's streaming read (drift_read_sum_f32x4) over gib_bytes."""
+    x = torch.ones(gib_bytes // 4, dtype=torch.float32, device=DEV)
+    partials = torch.empty(blocks, dtype=torch.float32, device=DEV)
+    probe = Kernel(name, f"read_sum_f32x4 over {gib_bytes >> 20} MiB, {blocks} blocks of 256", gib_bytes, 1, None, 1,
+                   read_bytes=gib_bytes)
+    probe.buffers = [(x, partials)]
+    probe.calls.append(("drift_read_sum_f32x4", lib.drift_read_sum_f32x4,
+                        (ctypes.c_void_p(x.data_ptr()), gib_bytes // 16, ctypes.c_void_p(partials.data_ptr()), blocks)))
+    return probe
+
+
+def time_graphs(kernels, steps: int, warmup: int) -> float:
+    """Each kernel's `steps` launches captured in a HIP graph (rotating its
+    buffer sets), replayed with one event pair around the replay on the
+    replaying stream: the average launch is the span over `steps`, with no
+    host call in it. Returns the wall time of all the replays."""
+    stream = torch.cuda.current_stream()
+    here = ctypes.c_void_p(stream.cuda_stream)
+    graphs = []
+    for k in kernels:
+        for i in range(warmup):
+            k.fire(i, here)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            captured = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+            for i in range(steps):
+                k.fire(warmup + i, captured)
+        graphs.append(g)
+    torch.cuda.synchronize()
+    for g in graphs:
+        g.replay()
+    torch.cuda.synchronize()
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in kernels]
+    t0 = time.perf_counter()
+    for g, (start, end) in zip(graphs, events):
+        start.record(stream)
+        g.replay()
+        end.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    for k, (start, end) in zip(kernels, events):
+        k.graph_ms = start.elapsed_time(end) / steps
+    del graphs
+    return wall
+
+
+def time_eager(kernels, steps: int) -> None:
+    """The same launches made one by one from Python through ctypes, as a
+    caller without graphs makes them: for launches shorter than the host's
+    call, the span includes the host."""
+    stream = torch.cuda.current_stream()
+    here = ctypes.c_void_p(stream.cuda_stream)
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in kernels]
+    torch.cuda.synchronize()
+    for k, (start, end) in zip(kernels, events):
+        start.record(stream)
+        for i in range(steps):
+            k.fire(i, here)
+        end.record(stream)
+    torch.cuda.synchronize()
+    for k, (start, end) in zip(kernels, events):
+        k.eager_ms = start.elapsed_time(end) / steps
+
+
+def host_call_cost() -> Optional[dict]:
+    """Host microseconds per C-ABI call, from drift_amd/host/launch_cost (a
+    C++ loop of 1000 calls of each entry point at its benchmark shape)."""
+    program = os.path.join(ROOT, "drift_amd", "host", "launch_cost")
+    if not os.path.exists(program):
+        return None
+    done = subprocess.run([program], capture_output=True, text=True, timeout=120)
+    if done.returncode != 0:
+        raise RuntimeError(f"launch_cost failed: {done.stdout}{done.stderr}")
+    return json.loads(done.stdout.strip().splitlines()[-1])
 
 
 # ------------------------------------------------------------------ main
@@ -523,6 +650,7 @@ def main():
         sys.exit(2)
 
     torch.cuda.set_device(0)
+    lib = _lib.load()
     hip = Prepared()
     kernels = make_kernels(hip)
     if args.only:
@@ -530,34 +658,48 @@ def main():
         kernels = [k for k in kernels if k.name in keep]
     for k in kernels:
         k.prepare(hip)
-    torch.cuda.synchronize()
-
+    # the ceilings: the stream probe at each long kernel's bytes and mix, and
+    # the reference's streaming read over 1 GiB (its 2048 blocks, and one pass)
+    probes = {}
     for k in kernels:
-        for i in range(args.warmup):
-            k.fire(i)
+        if k.bytes >= (8 << 20):
+            probes[k.name] = ceiling_probes(k, lib)
+    reads = [] if args.only else [read_probe(lib, 1 << 30, 2048, "read_sum_1gib_2048_blocks"),
+                                  read_probe(lib, 1 << 30, (1 << 30) // 16 // 1024, "read_sum_1gib_one_pass")]
     torch.cuda.synchronize()
 
-    # One event pair on the launch stream around each kernel's K back-to-back
-    # launches: the average launch duration is their span over K (a pair per
-    # launch would add the event's own dispatch to every launch, a few us).
-    stream = torch.cuda.current_stream()
-    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in kernels]
+    # kernels: graph replays (kernel time) and Python-driven launches (what a
+    # caller without graphs sees); the probes: graph replays
+    wall = time_graphs(kernels, args.steps, args.warmup)
+    time_eager(kernels, args.steps)
+    time_graphs([p for group in probes.values() for p in group] + reads, args.steps, args.warmup)
+    ceilings = {}
+    for k in kernels:
+        if k.name not in probes:
+            continue
+        best = min(probes[k.name], key=lambda p: p.graph_ms)
+        k.ceiling = best
+        gbs = best.bytes / (best.graph_ms * 1e-3) / 1e9
+        ceilings[k.name] = {"read_bytes": best.read_bytes, "write_bytes": best.bytes - best.read_bytes,
+                            "chunks_a_lane": best.per_lane, "us": round(best.graph_ms * 1e3, 2),
+                            "GB_s": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+                            "us_by_chunks_a_lane": {p.per_lane: round(p.graph_ms * 1e3, 2) for p in probes[k.name]}}
+    for r in reads:
+        gbs = r.bytes / (r.graph_ms * 1e-3) / 1e9
+        ceilings[r.name] = {"bytes": r.bytes, "us": round(r.graph_ms * 1e3, 2), "GB_s": round(gbs, 1),
+                            "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "what": r.config}
+    for group in probes.values():
+        for p in group:
+            p.buffers = None
+    for r in reads:
+        r.buffers = None
+    probes = reads = None
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for k, (start, end) in zip(kernels, events):
-        start.record(stream)
-        for i in range(args.steps):
-            k.fire(args.warmup + i)
-        end.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    for k, (start, end) in zip(kernels, events):
-        k.times_ms = [start.elapsed_time(end) / args.steps]
 
-    # The practical HBM ceiling on this box, measured in the same run: a plain
-    # device copy of one C5 tensor (402.6 MB read + 402.6 MB written) into
-    # two destinations in turn. It is also the known-size kernel that
+    # A plain device copy of one C5 tensor (402.6 MB read + 402.6 MB
+    # written) into two destinations in turn: the known-size kernel that
     # rocprofv3's FETCH_SIZE and WRITE_SIZE counts are scaled by.
+    stream = torch.cuda.current_stream()
     copy_elems = 65520 * 3072
     src = torch.empty(copy_elems, dtype=torch.bfloat16, device=DEV).fill_(1.0)
     dsts = [torch.empty_like(src) for _ in range(2)]
@@ -574,6 +716,8 @@ def main():
     copy_gbs = 2 * copy_elems * 2 / (copy_ms * 1e-3) / 1e9
     del src, dsts
 
+    host = None if args.only else host_call_cost()
+
     if not args.no_cpu:
         cpu_baseline(kernels, args.cpu_budget)
 
@@ -581,14 +725,17 @@ def main():
     ms_per_step = wall * 1e3 / args.steps
     table = {}
     for k in kernels:
-        avg = float(np.mean(k.times_ms))
+        avg = k.graph_ms
         gbs = k.bytes / (avg * 1e-3) / 1e9
         table[k.name] = {
-            "config": k.config, "us": round(avg * 1e3, 2), "bytes": k.bytes, "GB_s": round(gbs, 1),
-            "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "rows_per_s": round(k.rows / (avg * 1e-3), 1),
+            "config": k.config, "us": round(avg * 1e3, 2), "us_eager": round(k.eager_ms * 1e3, 2), "bytes": k.bytes,
+            "GB_s": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+            "rows_per_s": round(k.rows / (avg * 1e-3), 1),
         }
-    dominant = max(kernels, key=lambda k: np.mean(k.times_ms))
-    dom_avg = float(np.mean(dominant.times_ms))
+        if k.name in ceilings:
+            table[k.name]["frac_of_ceiling"] = round(gbs / ceilings[k.name]["GB_s"], 4)
+    dominant = max(kernels, key=lambda k: k.graph_ms)
+    dom_avg = dominant.graph_ms
     achieved = dominant.bytes / (dom_avg * 1e-3) / 1e9
     traffic = None
     traffic_file = os.path.join(ROOT, "profiles", "traffic.json")
@@ -615,10 +762,13 @@ def main():
                         "weights decoded to bf16 (Q4_K [14336,4096]; ConvRot int8 and 4-bit [13824,5120])",
             "step_bytes": step_bytes,
             "parallelism": "single GPU",
+            "timing": "each kernel's launches replayed from a captured HIP graph, one event pair per kernel",
         },
         "kernels": table,
+        "ceilings": ceilings,
         "hbm_copy_reference": {"GB_s": round(copy_gbs, 1), "frac_hbm_peak": round(copy_gbs / HBM_PEAK_GBS, 4),
-                               "what": "torch copy_ of 402.6 MB (read + write): the box's practical streaming ceiling"},
+                               "what": "torch copy_ of 402.6 MB (read + write)"},
+        "host_us_per_call": host,
         "roofline": {
             "kernel": dominant.name, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
             "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
@@ -631,8 +781,10 @@ def main():
         line["cpu_baseline"] = {
             "value": round(step_bytes / all_cores_s / 1e9, 4), "unit": "GB/s", "cores": host_threads(),
             "kind": "port",
-            "sample": "; ".join(f"{k.name}: {k.cpu[0]}, {k.cpu[1]:.4f} s a run on 1 core, "
-                                f"{k.cpu_all[1]:.4f} s on {k.cpu_all[0]}" for k in kernels),
+            "sample": "each kernel timed on a sample of its rows (the C4 ids gather from a full-size "
+                      "[151936, 4096] table) and scaled to the whole launch: "
+                      + "; ".join(f"{k.name}: {k.cpu[0]}, {k.cpu[1]:.4f} s a run on 1 core, "
+                                  f"{k.cpu_all[1]:.4f} s on {k.cpu_all[0]}" for k in kernels),
             "step_seconds": round(all_cores_s, 3),
             "single_core": {"value": round(step_bytes / one_core_s / 1e9, 4), "cores": 1,
                             "step_seconds": round(one_core_s, 2)},

@@ -76,9 +76,11 @@ SIGNATURES = {
     "drift_rotated_embedding_bf16": (_I32, [_P, _P, _I64, _P, _P, _I32, _P, _P, _I64, _I64, _I32, _P, _P]),
     "drift_rotated_dequantize_bf16": (_I32, [_P, _P, _I64, _P, _P, _I32, _P, _I64, _I32, _P]),
     "drift_convert": (_I32, [_P, _P, _I64, _I32, _P]),
+    "drift_read_sum_f32x4": (_I32, [_P, _I64, _P, _I32, _P]),
+    "drift_stream_mix": (_I32, [_P, _I64, _P, _I64, _I32, _P]),
 }
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 
 class NotBuilt(RuntimeError):

@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define DRIFT_ABI_VERSION 6
+#define DRIFT_ABI_VERSION 7
 
 /* Activation kinds: src/drift/runner/ops/Activation.scala:6-20. */
 enum {
@@ -419,6 +419,26 @@ int drift_rotated_dequantize_bf16(const void* codes, const float* scales, int64_
  * as tensor/DType.scala:105-115 decodes them). Replaces
  * kernels/elementwise.hip:68-86 convert (CPU ops/CpuMemory.scala:84-109). */
 int drift_convert(const void* x, void* out, int64_t n, int32_t kind, void* stream);
+
+/* ---------------------------------------------------------------- bandwidth probes
+ * drift_read_sum_f32x4: a streaming read of n4 float4 values (16-byte
+ * aligned x); block b writes the sum of the values it read to partials[b],
+ * for `blocks` blocks of 256 threads (at most 2^20). Each lane reads four
+ * float4 per pass over the grid, so blocks >= n4 / 1024 read everything in
+ * one pass. Replaces kernels/bandwidth.hip:5-20 read_sum_f32x4
+ * (runner/gpuTest/src/drift/runner/MemoryBandwidth.scala:37-52 launches it
+ * with 2048 blocks).
+ * drift_stream_mix: the read/write mix of a fused kernel, for its ceiling:
+ * read_chunks 16-byte chunks of src read and write_chunks (at least 1) of
+ * dst written, by 256-thread blocks that each read or write 256 x
+ * per_thread (1, 2 or 4) consecutive chunks, read and write blocks
+ * interleaved evenly in dispatch order; src and dst 16-byte aligned. dst
+ * gets a pattern of the chunk index (and its chunk 0 the fold of what a
+ * read block read, should that be all ones). No counterpart in the
+ * reference: its probe reads only. */
+int drift_read_sum_f32x4(const float* x, int64_t n4, float* partials, int32_t blocks, void* stream);
+int drift_stream_mix(const void* src, int64_t read_chunks, void* dst, int64_t write_chunks, int32_t per_thread,
+                     void* stream);
 
 #ifdef __cplusplus
 }

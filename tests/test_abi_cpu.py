@@ -23,7 +23,7 @@ def test_header_and_library_agree(lib):
 
 
 def test_version_and_error_text(lib):
-    assert lib.drift_abi_version() == _lib.ABI_VERSION == 6
+    assert lib.drift_abi_version() == _lib.ABI_VERSION == 7
     assert lib.drift_error_string(0).decode().lower().startswith("no error")
     assert lib.drift_error_string(1)
 
@@ -152,3 +152,12 @@ def test_rotated_tables_refuse_what_checkRotated_refuses(lib):
     assert "null ids" in refused(lib, "drift_rotated_embedding_f32", p, p, 4, NULL, NULL, 0, NULL, out, 3, 4, 256,
                                  NULL, NULL)
     assert lib.drift_rotated_embedding_bf16(NULL, NULL, 4, NULL, NULL, 0, NULL, NULL, 0, 4, 256, NULL, NULL) == 0
+
+
+def test_probes_refuse_bad_geometry(lib):
+    p = ctypes.c_void_p(16)
+    assert "0 blocks" in refused(lib, "drift_read_sum_f32x4", p, 100, p, 0, NULL)
+    assert "not 16-byte aligned" in refused(lib, "drift_read_sum_f32x4", ctypes.c_void_p(8), 100, p, 4, NULL)
+    assert "at least one written" in refused(lib, "drift_stream_mix", p, 10, p, 0, 1, NULL)
+    assert "3 a lane" in refused(lib, "drift_stream_mix", p, 10, p, 10, 3, NULL)
+    assert "null" in refused(lib, "drift_stream_mix", NULL, 10, p, 10, 1, NULL)
