@@ -15,6 +15,7 @@
 // 89-146, as rope.hpp), and F32 -> F16 rounding to nearest even for the
 // cache (Float.floatToFloat16 in ops/CpuAttention.scala:181-210).
 #include "rope.hpp"
+#include "sincos.hpp"
 
 #include <algorithm>
 #include <climits>
@@ -145,44 +146,42 @@ __global__ void __launch_bounds__(256) qk_norm_rope_kernel(const T* q, const T* 
   }
 }
 
-// The fast path for whole-chunk heads with every value turning: one block per
-// token, G lanes per head, each lane holding two chunks of its head (NeoX: a
-// chunk and its partner; otherwise chunks i and i + G), 64 / G heads per
-// wave. The grid covers the tokens in one pass. Each lane issues its loads
-// first; while they land the block makes the token's cos and sin (one sincos
-// per pair) and the norm weights (+ offset, in double) into LDS.
+// The fast path for whole-chunk heads with every value turning: one wave per
+// (token, group of 64 / G heads), each in a one-wave block, G lanes per head,
+// each lane holding two chunks of its head (NeoX: a chunk and its partner;
+// otherwise chunks i and i + G). The waves are independent: no block barrier.
+// A wave issues its loads first; while they land it makes its token's cos and
+// sin (a pair a lane, the double sin and cos of sincos.hpp) in its own LDS.
+// Heads with mRoPE sections (a position per section) take the general kernel.
 //
-// LDS is laid out so the G lanes of a head read consecutive entries: for NeoX
-// the pair (and weight) of lane i0's value i sits at i * G + i0 (the natural
-// index would put the G lanes N entries apart, on the same banks).
+// Measured on MI355X at Q [4096,32,128], K [4096,8,128] bf16, against the
+// designs it replaced: a block of five waves per token sharing the angles
+// through a barrier 17.5 us, a wave per token (all 40 heads) 19.3 us, two
+// tokens a wave 17.5 us, 16 lanes a head (one chunk a lane, partners by DPP)
+// 21.5 us; this one 15.7 us. One-wave blocks stream faster than larger ones at
+// this size: a plain copy of the same bytes takes 14.3 us in one-wave blocks
+// and 15.5 us in 256-thread blocks.
+//
+// The angles' LDS is laid out so the G lanes of a head read consecutive
+// entries: for NeoX the pair of lane i0's value i sits at i * G + i0 (the
+// natural index would put the G lanes N entries apart, on the same banks).
 template <bool NEOX, int G, int N>
 __device__ __forceinline__ int qk_pair_slot(int pair) {
   if constexpr (NEOX) return (pair % N) * G + pair / N;
   return pair;
 }
 
-template <bool NEOX, int G, int N>
-__device__ __forceinline__ int qk_weight_slot(int d) {
-  if constexpr (NEOX) {
-    const int half = N * G;
-    const int h = d >= half ? 1 : 0, e = d - h * half;
-    return h * half + (e % N) * G + e / N;
-  }
-  return d;
-}
-
-// Values into the cache by tiles: a tile is 16 consecutive positions of one
-// page (16 divides the page size) for one key head. The tile's values load
-// as chunks of N, go to LDS transposed ([value][position]) as F16, and leave
-// as 16-byte stores of 8 positions of one value: in the value layout
-// ([page][head][value][position]) a whole tile of a 16-token page is one
-// contiguous run. A position the tokens do not cover is left alone; a tile
-// of a page outside the cache writes nothing and sets *bad_page.
-constexpr int kQkMinThreads(int dim) { return dim < 64 ? 64 : (dim + 63) / 64 * 64; }
-
+// Values into the cache by tiles, one tile a one-wave block: a tile is 16
+// consecutive positions of one page (16 divides the page size) for H key
+// heads. The tile's values load as chunks of N, go to LDS transposed
+// ([value][position]) as F16, and leave as 16-byte stores of 8 positions of
+// one value: in the value layout ([page][head][value][position]) a whole tile
+// of a 16-token page is one contiguous run. A position the tokens do not
+// cover is left alone; a tile of a page outside the cache writes nothing and
+// sets *bad_page.
+//
 // Key heads per value tile: as many as keep the staged tile within 4 KiB of
-// LDS (one head of 128; larger tiles measured slower, the kernel's LDS
-// holding fewer token blocks per CU).
+// LDS (one head of 128).
 constexpr int kTileHeads(int dim) { return dim * 32 >= 4096 ? 1 : 4096 / (dim * 32); }
 
 template <typename T, int DIM, int H = kTileHeads(DIM)>
@@ -190,189 +189,229 @@ __device__ __forceinline__ void cache_values_tile(const Extras<T>& e, int64_t to
   constexpr int N = Chunk<T>::N;
   constexpr int kTile = 16;
   constexpr int kChunks = kTile * H * (DIM / N);
+  constexpr int kRound = 4;  // chunks a lane has in flight
   __shared__ __align__(16) uint16_t staged[H][DIM][kTile];
+  const int lane = threadIdx.x;
   const int head_blocks = (kv_heads + H - 1) / H;
   const int kv0 = (int)(tile % head_blocks) * H;
   const int heads = min(H, kv_heads - kv0);
   const int64_t first = (e.start / kTile + tile / head_blocks) * kTile;  // the tile's first position
   const int64_t lo = max(first, (int64_t)e.start), hi = min(first + kTile, e.start + tokens);
-  // the values load first (their addresses do not need the page), positions
-  // the tokens do not cover and heads past the last clamped to ones they do
-  // (a launch's blocks have at least max(64, DIM) threads)
-  constexpr int kPerThread = (kChunks + kQkMinThreads(DIM) - 1) / kQkMinThreads(DIM);
-  typename Chunk<T>::Raw raw[kPerThread];
+  const int64_t page = e.page_table[first / e.page_size];
+  // the values load kRound chunks a lane at a time; positions the tokens do
+  // not cover and heads past the last are clamped to ones they do
+  for (int base = 0; base < kChunks; base += kRound * kWave) {
+    typename Chunk<T>::Raw raw[kRound];
 #pragma unroll
-  for (int r = 0; r < kPerThread; ++r) {
-    const int c = (int)threadIdx.x + r * (int)blockDim.x;
-    if (c < kChunks) {
+    for (int r = 0; r < kRound; ++r) {
+      const int c = min(base + r * kWave + lane, kChunks - 1);
       const int i = c / (H * (DIM / N)), hh = min(c / (DIM / N) % H, heads - 1), d = (c % (DIM / N)) * N;
       const int64_t position = min(max(first + i, lo), hi - 1);
       raw[r] = Chunk<T>::load_raw(e.v + ((position - e.start) * kv_heads + kv0 + hh) * DIM + d);
     }
-  }
-  const int64_t page = e.page_table[first / e.page_size];
 #pragma unroll
-  for (int r = 0; r < kPerThread; ++r) {
-    const int c = (int)threadIdx.x + r * (int)blockDim.x;
-    if (c >= kChunks) break;
-    const int i = c / (H * (DIM / N)), hh = c / (DIM / N) % H, d = (c % (DIM / N)) * N;
-    float v[N];
-    Chunk<T>::unpack(raw[r], v);
+    for (int r = 0; r < kRound; ++r) {
+      const int c = base + r * kWave + lane;
+      if (c >= kChunks) break;
+      const int i = c / (H * (DIM / N)), hh = c / (DIM / N) % H, d = (c % (DIM / N)) * N;
+      float v[N];
+      Chunk<T>::unpack(raw[r], v);
 #pragma unroll
-    for (int j = 0; j < N; ++j) staged[hh][d + j][i] = (uint16_t)f16_bits(v[j]);
+      for (int j = 0; j < N; ++j) staged[hh][d + j][i] = (uint16_t)f16_bits(v[j]);
+    }
   }
-  __syncthreads();
+  wave_sync();
   if (page < 0 || page >= e.pages) {
-    if (e.bad_page && threadIdx.x == 0) *e.bad_page = 1;
+    if (e.bad_page && lane == 0) *e.bad_page = 1;
     return;
   }
   // rows (head, value) of the tile: kv0's row 0, then on, page_size apart
   uint16_t* row0 = e.values + (page * kv_heads + kv0) * (int64_t)DIM * e.page_size + first % e.page_size;
   if (lo == first && hi == first + kTile) {
-    for (int c = threadIdx.x; c < heads * DIM * 2; c += blockDim.x) {
+    for (int c = lane; c < heads * DIM * 2; c += kWave) {
       const int row = c / 2, i = (c % 2) * 8;
       const uint4 w = *reinterpret_cast<const uint4*>(&staged[row / DIM][row % DIM][i]);
       *reinterpret_cast<uint4*>(row0 + (int64_t)row * e.page_size + i) = w;
     }
   } else {
-    for (int c = threadIdx.x; c < heads * DIM * kTile; c += blockDim.x) {
+    for (int c = lane; c < heads * DIM * kTile; c += kWave) {
       const int row = c / kTile, i = c % kTile;
       if (first + i >= lo && first + i < hi) row0[(int64_t)row * e.page_size + i] = staged[row / DIM][row % DIM][i];
     }
   }
 }
 
-constexpr int kQkMaxWaves = 16;
+// 1 / sqrt(m) by the hardware's reciprocal square root and two Newton steps
+// (within a double ulp or two of the correctly rounded quotient of the
+// correctly rounded root, which moves an F32 result only where it lies that
+// close to a rounding boundary). Without a branch: a subnormal m is scaled
+// into range first (2^256 m, the result times 2^128), and 0 and infinity give
+// the division's own infinity and zero; NaN stays NaN.
+__device__ __forceinline__ double inverse_sqrt(double m) {
+  const bool tiny = m < 0x1p-1000;
+  const double ms = tiny ? m * 0x1p256 : m;
+  double y = __builtin_amdgcn_rsq(ms);
+  y = y * fma(-0.5 * ms * y, y, 1.5);
+  y = y * fma(-0.5 * ms * y, y, 1.5);
+  y = tiny ? y * 0x1p128 : y;
+  y = m == 0.0 ? __builtin_huge_val() : y;
+  return m == __builtin_huge_val() ? 0.0 : y;
+}
 
-template <typename T, int G, bool NEOX, bool EXTRAS>
-__global__ void __launch_bounds__(kQkMaxWaves * 64) qk_norm_rope_token(const T* q, const T* k, T* q_out, T* k_out,
-                                                                     const float* q_weight, const float* k_weight,
-                                                                     const int32_t* positions, QkArgs a,
-                                                                     Extras<T> e) {
+template <typename T, int G, bool NEOX, bool EXTRAS, bool UNIFORM>
+__device__ __forceinline__ void qk_wave_heads(const T* q, const T* k, T* q_out, T* k_out, const float* q_weight,
+                                              const float* k_weight, const int32_t* positions, const QkArgs& a,
+                                              const Extras<T>& e, int64_t t, int group) {
   constexpr int N = Chunk<T>::N;
   using Raw = typename Chunk<T>::Raw;
   constexpr int kHeadsPerWave = kWave / G;
-  constexpr int kPairs = N * G;  // a head's pairs (rotary == dim == 2 N G)
-  __shared__ double2 cs[kPairs];
-  __shared__ double weights[2][2 * kPairs];
+  constexpr int dim = 2 * N * G, half = N * G;  // a head's pairs: half (rotary == dim)
+  __shared__ double2 cs[half];
   const RopeArgs& p = a.rope;
-  constexpr int dim = 2 * N * G, half = N * G;
-  const int64_t t = blockIdx.x;
-  if constexpr (EXTRAS) {
-    // with the cache, blocks past the tokens' write the values by tiles
-    if (t >= p.tokens) {
-      cache_values_tile<T, dim>(e, p.tokens, a.kv_heads, t - p.tokens);
-      return;
-    }
-  }
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int waves = blockDim.x >> 6;
+  const int lane = threadIdx.x;
   const int rows = a.q_heads + a.kv_heads;
   const int i0 = lane % G;
   const int d0 = i0 * N, d1 = (NEOX ? half : G * N) + i0 * N;
-  auto head_at = [&](auto* qs, auto* ks, int h) {
-    return h < a.q_heads ? qs + (t * a.q_heads + h) * dim : ks + (t * a.kv_heads + (h - a.q_heads)) * dim;
-  };
-  auto input_at = [&](int h) {
-    return h < a.q_heads ? q + (t * a.q_heads + h) * a.q_stride : k + (t * a.kv_heads + (h - a.q_heads)) * dim;
-  };
-  // the angles' and weights' operands load first: a wave's loads complete in
-  // issue order, so the tables are made while the heads are still loading
-  const int j = threadIdx.x, jp = min(j, half - 1), jd = min(j, dim - 1);
-  const int32_t position = positions[(int64_t)rope_section(jp, p) * p.tokens + t];
-  const float inverse = p.inverse[jp];
-  const float qw = q_weight[jd], kw = k_weight[jd];
-  // loads are never branched around (the wait for the angles' operands would
-  // then wait for them too): a head past the last is clamped to it
-  int h = wave * kHeadsPerWave + lane / G;
-  const T* xh = input_at(min(h, rows - 1));
-  Raw r0 = Chunk<T>::load_raw(xh + d0);
-  Raw r1 = Chunk<T>::load_raw(xh + d1);
-  // the gate half of a query head's row (rows past the last query head are
-  // clamped to it)
+  const int h = group * kHeadsPerWave + lane / G;
+  const bool live = h < rows;
+  // UNIFORM: the wave's heads are all queries or all keys, so the choice of
+  // tensor (and its addresses' base) is the wave's, not each lane's
+  const bool query = UNIFORM ? group * kHeadsPerWave < a.q_heads : h < a.q_heads;
+  // the small operands load first (the token's position, the pairs'
+  // frequencies, the lane's norm weights), then the heads: loads complete in
+  // order, so waiting for the small ones never waits for the heads, and the
+  // angles are made while the heads land. A head past the last is clamped to
+  // it (loads are never branched around). Measured at the C3 shape, against
+  // weights staged as doubles in LDS, a position read per lane and a branch
+  // for irregular sums: each of those cost about 1 us.
+  constexpr int kPairsPerLane = (half + kWave - 1) / kWave;
+  const int32_t position = positions[t];  // single-section rope: one position a token
+  float inverse[kPairsPerLane];
+#pragma unroll
+  for (int u = 0; u < kPairsPerLane; ++u) inverse[u] = p.inverse[min(lane + u * kWave, half - 1)];
+  const int hc = min(h, rows - 1);
+  const bool query_c = UNIFORM ? query : hc < a.q_heads;
+  const float* ws = query_c ? q_weight : k_weight;
+  float w0[N], w1[N];
+#pragma unroll
+  for (int i = 0; i < N; i += 4) {
+    const float4 x0 = *reinterpret_cast<const float4*>(ws + d0 + i), x1 = *reinterpret_cast<const float4*>(ws + d1 + i);
+    w0[i] = x0.x, w0[i + 1] = x0.y, w0[i + 2] = x0.z, w0[i + 3] = x0.w;
+    w1[i] = x1.x, w1[i + 1] = x1.y, w1[i + 2] = x1.z, w1[i + 3] = x1.w;
+  }
+  const T* xh = query_c ? q + (t * a.q_heads + hc) * a.q_stride : k + (t * a.kv_heads + (hc - a.q_heads)) * dim;
+  const Raw r0 = Chunk<T>::load_raw(xh + d0);
+  const Raw r1 = Chunk<T>::load_raw(xh + d1);
+  // the gate half of a query head's row (key heads clamped to the last query head)
   Raw g0, g1;
-  auto load_extras = [&](int hh) {
+  if constexpr (EXTRAS) {
     if (e.gate && a.q_heads > 0) {
-      const T* gh = q + (t * a.q_heads + min(hh, a.q_heads - 1)) * a.q_stride + dim;
+      const T* gh = q + (t * a.q_heads + min(hc, a.q_heads - 1)) * a.q_stride + dim;
       g0 = Chunk<T>::load_raw(gh + d0);
       g1 = Chunk<T>::load_raw(gh + d1);
     }
-  };
-  if constexpr (EXTRAS) load_extras(h);
-  if (j < half) {
-    double sn, cn;
-    sincos((double)((float)position * inverse), &sn, &cn);
-    cs[qk_pair_slot<NEOX, G, N>(j)] = make_double2(cn, sn);
   }
-  if (j < dim) {
-    const int slot = qk_weight_slot<NEOX, G, N>(j);
-    weights[0][slot] = (double)qw + (double)a.offset;
-    weights[1][slot] = (double)kw + (double)a.offset;
-  }
-  __syncthreads();
-  for (;;) {
-    const bool live = h < rows;
-    float v0[N], v1[N];
-    double squares = 0.0;
-    if (live) {
-      Chunk<T>::unpack(r0, v0);
-      Chunk<T>::unpack(r1, v1);
+  // the token's cos and sin, a pair a lane, into the wave's LDS
 #pragma unroll
-      for (int i = 0; i < N; ++i) {
-        squares = fma((double)v0[i], (double)v0[i], squares);
-        squares = fma((double)v1[i], (double)v1[i], squares);
-      }
+  for (int u = 0; u < kPairsPerLane; ++u) {
+    const int j = lane + u * kWave;
+    if (j < half) {
+      const float angle = (float)position * inverse[u];
+      double sn, cn;
+      if (!sincos_reduced(angle, &sn, &cn)) sincos((double)angle, &sn, &cn);
+      cs[qk_pair_slot<NEOX, G, N>(j)] = make_double2(cn, sn);
     }
-    squares = group_sum<G>(squares);
-    if (live) {
-      const double factor = 1.0 / sqrt(squares / (double)dim + (double)a.eps);
-      const double* w = weights[h < a.q_heads ? 0 : 1];
-#pragma unroll
-      for (int i = 0; i < N; ++i) {
-        v0[i] = (float)((double)v0[i] * factor * w[qk_weight_slot<NEOX, G, N>(d0 + i)]);
-        v1[i] = (float)((double)v1[i] * factor * w[qk_weight_slot<NEOX, G, N>(d1 + i)]);
-      }
-      if constexpr (NEOX) {
-#pragma unroll
-        for (int i = 0; i < N; ++i) {
-          const double2 c = cs[qk_pair_slot<NEOX, G, N>(d0 + i)];
-          turn_fused(v0[i], v1[i], c.x, c.y, v0[i], v1[i]);
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < N; i += 2) {
-          const double2 c0 = cs[(d0 + i) / 2], c1 = cs[(d1 + i) / 2];
-          turn_fused(v0[i], v0[i + 1], c0.x, c0.y, v0[i], v0[i + 1]);
-          turn_fused(v1[i], v1[i + 1], c1.x, c1.y, v1[i], v1[i + 1]);
-        }
-      }
-      const bool query = h < a.q_heads;
-      if (!EXTRAS || query || !e.keys) {
-        T* oh = head_at(q_out, k_out, h);
-        Chunk<T>::store(oh + d0, v0);
-        Chunk<T>::store(oh + d1, v1);
-      }
-      if constexpr (EXTRAS) {
-        if (query && e.gate) {
-          T* gh = e.gate + (t * a.q_heads + h) * dim;
-          *reinterpret_cast<uint4*>(gh + d0) = g0;
-          *reinterpret_cast<uint4*>(gh + d1) = g1;
-        }
-        int64_t key, value;
-        if (!query && e.keys && cache_place(e, t, a.kv_heads, dim, h - a.q_heads, key, value)) {
-          store_f16<N>(e.keys + key + d0, v0);
-          store_f16<N>(e.keys + key + d1, v1);
-        }
-      }
-    }
-    // more heads than the block has waves for: the next pass of this wave
-    h += waves * kHeadsPerWave;
-    if (h - lane / G >= rows) break;
-    xh = input_at(min(h, rows - 1));
-    r0 = Chunk<T>::load_raw(xh + d0);
-    r1 = Chunk<T>::load_raw(xh + d1);
-    if constexpr (EXTRAS) load_extras(h);
   }
+  wave_sync();
+  float v0[N], v1[N];
+  Chunk<T>::unpack(r0, v0);
+  Chunk<T>::unpack(r1, v1);
+  double squares = 0.0;
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    squares = fma((double)v0[i], (double)v0[i], squares);
+    squares = fma((double)v1[i], (double)v1[i], squares);
+  }
+  squares = group_sum<G>(squares);
+  const double factor = inverse_sqrt(squares / (double)dim + (double)a.eps);
+  // (double) weight + offset, as the reference adds them; with no offset
+  // the addition is an identity and is skipped
+  if (a.offset != 0.0f) {
+    const double offset = (double)a.offset;
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      v0[i] = (float)((double)v0[i] * factor * ((double)w0[i] + offset));
+      v1[i] = (float)((double)v1[i] * factor * ((double)w1[i] + offset));
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      v0[i] = (float)((double)v0[i] * factor * (double)w0[i]);
+      v1[i] = (float)((double)v1[i] * factor * (double)w1[i]);
+    }
+  }
+  if constexpr (NEOX) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const double2 c = cs[qk_pair_slot<NEOX, G, N>(d0 + i)];
+      turn_fused(v0[i], v1[i], c.x, c.y, v0[i], v1[i]);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; i += 2) {
+      const double2 c0 = cs[(d0 + i) / 2], c1 = cs[(d1 + i) / 2];
+      turn_fused(v0[i], v0[i + 1], c0.x, c0.y, v0[i], v0[i + 1]);
+      turn_fused(v1[i], v1[i + 1], c1.x, c1.y, v1[i], v1[i + 1]);
+    }
+  }
+  if (!live) return;
+  if (!EXTRAS || query || !e.keys) {
+    T* oh = query ? q_out + (t * a.q_heads + h) * dim : k_out + (t * a.kv_heads + (h - a.q_heads)) * dim;
+    Chunk<T>::store(oh + d0, v0);
+    Chunk<T>::store(oh + d1, v1);
+  }
+  if constexpr (EXTRAS) {
+    if (query && e.gate) {
+      T* gh = e.gate + (t * a.q_heads + h) * dim;
+      *reinterpret_cast<uint4*>(gh + d0) = g0;
+      *reinterpret_cast<uint4*>(gh + d1) = g1;
+    }
+    int64_t key, value;
+    if (!query && e.keys && cache_place(e, t, a.kv_heads, dim, h - a.q_heads, key, value)) {
+      store_f16<N>(e.keys + key + d0, v0);
+      store_f16<N>(e.keys + key + d1, v1);
+    }
+  }
+}
+
+template <typename T, int G, bool NEOX, bool EXTRAS>
+__global__ void __launch_bounds__(kWave) qk_norm_rope_wave(const T* q, const T* k, T* q_out, T* k_out,
+                                                          const float* q_weight, const float* k_weight,
+                                                          const int32_t* positions, QkArgs a, Extras<T> e,
+                                                          int waves_per_token) {
+  constexpr int N = Chunk<T>::N;
+  constexpr int kHeadsPerWave = kWave / G;
+  constexpr int dim = 2 * N * G;
+  const RopeArgs& p = a.rope;
+  const int64_t item = blockIdx.x;
+  if constexpr (EXTRAS) {
+    // with the cache, blocks past the tokens' waves write the values by tiles
+    if (item >= p.tokens * (int64_t)waves_per_token) {
+      cache_values_tile<T, dim>(e, p.tokens, a.kv_heads, item - p.tokens * (int64_t)waves_per_token);
+      return;
+    }
+  }
+  // blocks number fewer than 2^31 (the launcher checks): 32-bit division
+  const uint32_t token = (uint32_t)item / (uint32_t)waves_per_token;
+  const int64_t t = token;
+  const int group = (int)((uint32_t)item - token * (uint32_t)waves_per_token);
+  // a wave whose heads are all queries or all keys (every wave, when the
+  // query heads fill whole waves) takes the wave-uniform addressing
+  const int first = group * kHeadsPerWave;
+  if (first + kHeadsPerWave <= a.q_heads || first >= a.q_heads)
+    qk_wave_heads<T, G, NEOX, EXTRAS, true>(q, k, q_out, k_out, q_weight, k_weight, positions, a, e, t, group);
+  else
+    qk_wave_heads<T, G, NEOX, EXTRAS, false>(q, k, q_out, k_out, q_weight, k_weight, positions, a, e, t, group);
 }
 
 // ------------------------------------------------------------------ cache write, split halves
@@ -460,33 +499,33 @@ int qk_launch(const char* entry, const T* q, const T* k, T* q_out, T* k_out, con
   const int dim = p.dim;
   const int lanes_per_head = dim / (2 * N);
   const bool whole = p.rotary == dim && dim % (2 * N) == 0 && (lanes_per_head & (lanes_per_head - 1)) == 0 &&
-                     lanes_per_head <= kWave / 2 && aligned;
+                     lanes_per_head <= kWave / 2 && aligned && p.sections == DRIFT_SECTIONS_SINGLE;
   if (!whole) {
     hipLaunchKernelGGL((qk_norm_rope_kernel<T, EXTRAS>), dim3(grid_for(p.tokens, 1, 1 << 16)), dim3(256), 0, st, q,
                        k, q_out, k_out, q_weight, k_weight, positions, a, e);
     return launched(entry);
   }
+  // a one-wave block per (token, group of 64 / G heads); with the cache,
+  // blocks past those write the values by tiles of 16 positions
   const int heads_per_wave = kWave / lanes_per_head;
-  // a wave per 64 / G heads, and a thread per weight of a head
-  const int waves = (int)std::min<int64_t>(
-      kQkMaxWaves, std::max<int64_t>(ceil_div(a.q_heads + a.kv_heads, heads_per_wave), ceil_div(dim, kWave)));
-  // with the cache, blocks past the tokens write the values by tiles of 16
-  // positions and one key head
+  const int waves_per_token = (int)ceil_div(a.q_heads + a.kv_heads, heads_per_wave);
   Extras<T> ex = e;
   const int tile_heads = kTileHeads(dim);
   ex.tiles = EXTRAS && e.keys ? ((int64_t)(e.start + p.tokens - 1) / 16 - e.start / 16 + 1) *
                                     ((a.kv_heads + tile_heads - 1) / tile_heads)
                               : 0;
-  const dim3 grid((unsigned)(p.tokens + ex.tiles)), block(64 * waves);
+  const int64_t blocks = (int64_t)p.tokens * waves_per_token + ex.tiles;
+  if (blocks > INT32_MAX) return refuse("%s: %d tokens of %d heads", entry, p.tokens, a.q_heads + a.kv_heads);
+  const dim3 grid((unsigned)blocks), block(kWave);
   switch (lanes_per_head) {
 #define DRIFT_QK_CASE(G)                                                                                             \
   case G:                                                                                                            \
     if (p.layout == DRIFT_ROPE_NEOX)                                                                                 \
-      hipLaunchKernelGGL((qk_norm_rope_token<T, G, true, EXTRAS>), grid, block, 0, st, q, k, q_out, k_out, q_weight, \
-                         k_weight, positions, a, ex);                                                                 \
+      hipLaunchKernelGGL((qk_norm_rope_wave<T, G, true, EXTRAS>), grid, block, 0, st, q, k, q_out, k_out, q_weight,  \
+                         k_weight, positions, a, ex, waves_per_token);                                                \
     else                                                                                                             \
-      hipLaunchKernelGGL((qk_norm_rope_token<T, G, false, EXTRAS>), grid, block, 0, st, q, k, q_out, k_out,          \
-                         q_weight, k_weight, positions, a, ex);                                                       \
+      hipLaunchKernelGGL((qk_norm_rope_wave<T, G, false, EXTRAS>), grid, block, 0, st, q, k, q_out, k_out,           \
+                         q_weight, k_weight, positions, a, ex, waves_per_token);                                      \
     break;
     DRIFT_QK_CASE(1)
     DRIFT_QK_CASE(2)
