@@ -5,6 +5,7 @@
 #pragma once
 
 #include <cmath>
+#include <cstring>
 
 #include "common.hpp"
 
@@ -121,6 +122,27 @@ inline int check_rope(const char* entry, int32_t tokens, int32_t heads, int32_t 
 
 // The inverse frequencies as the CPU reference makes them
 // (ops/CpuAttention.scala:124-133).
+inline void make_inverse(float (&inverse)[kMaxPairs], int32_t rotary, float theta, int32_t sections,
+                         const int32_t (&s)[4]) {
+  for (int pair = 0; pair < kMaxPairs; ++pair) {
+    if (pair >= rotary / 2) {
+      inverse[pair] = 0.0f;
+      continue;
+    }
+    double exponent = 2.0 * pair / (double)rotary;
+    if (sections == DRIFT_SECTIONS_AXES) {
+      int start = 0, axis = 0;
+      while (pair >= start + s[axis]) start += s[axis++];
+      exponent = (double)(pair - start) / (double)s[axis];
+    }
+    inverse[pair] = 1.0f / (float)std::pow((double)theta, exponent);
+  }
+}
+
+// A launch's rope arguments. The inverse frequencies depend only on (theta,
+// rotary, sections and their sizes), which a model keeps for every layer, so
+// each host thread keeps those of its last four configurations: a decode
+// step's launches copy the table instead of taking up to 256 pow calls.
 inline void fill_rope(RopeArgs& p, int32_t tokens, int32_t heads, int32_t dim, int32_t rotary, float theta, int32_t layout,
                int32_t sections, const int32_t (&s)[4]) {
   p.tokens = tokens;
@@ -130,19 +152,34 @@ inline void fill_rope(RopeArgs& p, int32_t tokens, int32_t heads, int32_t dim, i
   p.layout = layout;
   p.sections = sections;
   for (int a = 0; a < 4; ++a) p.s[a] = s[a];
-  for (int pair = 0; pair < kMaxPairs; ++pair) {
-    if (pair >= rotary / 2) {
-      p.inverse[pair] = 0.0f;
-      continue;
+  struct Tables {
+    struct Key {
+      float theta;
+      int32_t rotary, sections, s[4];
+    } key;
+    float inverse[kMaxPairs];
+    bool used;
+  };
+  constexpr int kKept = 4;
+  thread_local Tables kept[kKept] = {};
+  thread_local int next = 0;
+  Tables::Key key;
+  std::memset(&key, 0, sizeof key);  // no padding left undefined for the comparison
+  key.theta = theta;
+  key.rotary = rotary;
+  key.sections = sections;
+  for (int a = 0; a < 4; ++a) key.s[a] = s[a];
+  for (Tables& t : kept)
+    if (t.used && std::memcmp(&t.key, &key, sizeof key) == 0) {
+      std::memcpy(p.inverse, t.inverse, sizeof p.inverse);
+      return;
     }
-    double exponent = 2.0 * pair / (double)rotary;
-    if (sections == DRIFT_SECTIONS_AXES) {
-      int start = 0, axis = 0;
-      while (pair >= start + s[axis]) start += s[axis++];
-      exponent = (double)(pair - start) / (double)s[axis];
-    }
-    p.inverse[pair] = 1.0f / (float)std::pow((double)theta, exponent);
-  }
+  Tables& t = kept[next];
+  next = (next + 1) % kKept;
+  t.key = key;
+  make_inverse(t.inverse, rotary, theta, sections, s);
+  t.used = true;
+  std::memcpy(p.inverse, t.inverse, sizeof p.inverse);
 }
 
 }  // namespace

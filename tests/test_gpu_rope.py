@@ -66,6 +66,24 @@ def test_reference_rope_configurations(hip, index):
     assert_bf16(o.to_bf16(oracle_rope(o.from_bf16(xb), positions, rope)), host_bits(outb), what=f"rope bf16 {index}")
 
 
+def test_rope_tables_follow_the_configuration(hip):
+    # the library keeps the inverse frequencies of its last four rope
+    # configurations per host thread: alternating between six (each theta,
+    # rotary width and section split a different table) twice over, every
+    # call must use its own
+    step("rope f32 over six configurations, twice")
+    ropes = REFERENCE_ROPES[:2] + REFERENCE_ROPES[3:5] + REFERENCE_ROPES[5:7]
+    x = gaussian(3, (37, 3, 256), 2.0)
+    for round_ in range(2):
+        for index, rope in enumerate(ropes):
+            dimension = 256 if rope.rotaryDimensions == 64 else 128
+            shape, positions = reference_case(rope)
+            xs = np.ascontiguousarray(x[:, :, :dimension])
+            out = torch.empty(shape, dtype=torch.float32, device=DEV)
+            hip.rope(dev_f32(xs), dev_i32(positions), rope, out)
+            assert_f32(oracle_rope(xs, positions, rope), host_f32(out), what=f"round {round_}, rope {index}")
+
+
 @pytest.mark.parametrize("shape,rotary,layout", [((5, 2, 6), 2, 0), ((4, 3, 10), 6, 1), ((3, 2, 7), 4, 0),
                                                  ((6, 5, 96), 48, 0), ((2, 1, 512), 512, 1)])
 def test_rope_odd_shapes_and_in_place(hip, shape, rotary, layout):
