@@ -31,7 +31,9 @@ and writes of the tensors each op names) over the step's wall time;
 `kernels` has each kernel's HIP-event time, GB/s, fraction of the 8 TB/s HBM
 peak, fraction of its ceiling and rows/s; `ceilings` is the streaming probe
 (drift_stream_mix) moving each long kernel's bytes in its read:write mix,
-and the reference's streaming read (drift_read_sum_f32x4) over 1 GiB;
+for the gather also its own pattern with no decode (drift_row_probe: the
+rows its ids name read, its output written; `frac_of_row_probe`), and the
+reference's streaming read (drift_read_sum_f32x4) over 1 GiB;
 `roofline` is the dominant kernel's; `cpu_baseline` is the CPU reference
 arithmetic (the oracle) timed on a bounded sample of the same work on this
 host's cores, scaled to the whole step.
@@ -243,7 +245,9 @@ def make_kernels(hip: d.HipOps):
         table[lo:hi, :, 0:2] = sc.view(torch.uint8).view(hi - lo, blocks, 2)
     q8 = d.Q8_0Table(table.view(vocab, blocks * 34), cols)
     nbytes = count * blocks * 34 + count * 4 + count * cols * 2
-    n = sets_for(nbytes)
+    # id sets enough that the rows they name total more than 512 MB: fewer
+    # sets would re-read rows the 256 MB MALL still holds from earlier sets
+    n = sets_for(count * blocks * 34)
     idss = [torch.randint(0, vocab, (count,), generator=gen(500 + i), device=DEV, dtype=torch.int32)
             for i in range(n)]
     gouts = [torch.empty((count, cols), dtype=torch.bfloat16, device=DEV) for _ in range(n)]
@@ -554,6 +558,24 @@ def ceiling_probes(k: Kernel, lib) -> list:
     return probes
 
 
+def row_probe(k: Kernel, lib) -> Kernel:
+    """The gather's own pattern with no decode (drift_row_probe): each of
+    k's launches (table, ids, out, count, vocab, cols, bad_id) becomes a
+    block per id reading the whole Q8_0 row the id names and writing the
+    row's BF16 bytes, with the same ids and outputs. Random rows of a table
+    larger than the cache come from scattered DRAM pages, which the stream
+    probe's contiguous reads do not measure."""
+    probe = Kernel(f"row probe of {k.name}", "rows of the gather's table read at its ids, its output written",
+                   k.bytes, k.rows, None, k.sets, read_bytes=k.read_bytes)
+    for _, _, (table, ids, out, count, vocab, cols, _) in k.calls:
+        row_bytes = cols // 32 * 34
+        if row_bytes % 16 or table.value % 16:
+            return None
+        probe.calls.append(("drift_row_probe", lib.drift_row_probe,
+                            (table, vocab, row_bytes // 16, ids, count, out, cols * 2 // 16)))
+    return probe
+
+
 def read_probe(lib, gib_bytes: int, blocks: int, name: str) -> Kernel:
     """The reference's streaming read (drift_read_sum_f32x4) over gib_bytes."""
     x = torch.ones(gib_bytes // 4, dtype=torch.float32, device=DEV)
@@ -664,6 +686,12 @@ def main():
     for k in kernels:
         if k.bytes >= (8 << 20):
             probes[k.name] = ceiling_probes(k, lib)
+    rows_probes = {}
+    for k in kernels:
+        if k.name == "embedding_q8_0_bf16":
+            p = row_probe(k, lib)
+            if p is not None:
+                rows_probes[k.name] = p
     reads = [] if args.only else [read_probe(lib, 1 << 30, 2048, "read_sum_1gib_2048_blocks"),
                                   read_probe(lib, 1 << 30, (1 << 30) // 16 // 1024, "read_sum_1gib_one_pass")]
     torch.cuda.synchronize()
@@ -672,7 +700,8 @@ def main():
     # caller without graphs sees); the probes: graph replays
     wall = time_graphs(kernels, args.steps, args.warmup)
     time_eager(kernels, args.steps)
-    time_graphs([p for group in probes.values() for p in group] + reads, args.steps, args.warmup)
+    time_graphs([p for group in probes.values() for p in group] + list(rows_probes.values()) + reads, args.steps,
+                args.warmup)
     ceilings = {}
     for k in kernels:
         if k.name not in probes:
@@ -684,6 +713,10 @@ def main():
                             "chunks_a_lane": best.per_lane, "us": round(best.graph_ms * 1e3, 2),
                             "GB_s": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
                             "us_by_chunks_a_lane": {p.per_lane: round(p.graph_ms * 1e3, 2) for p in probes[k.name]}}
+    for name, p in rows_probes.items():
+        gbs = p.bytes / (p.graph_ms * 1e-3) / 1e9
+        ceilings[name]["row_probe"] = {"us": round(p.graph_ms * 1e3, 2), "GB_s": round(gbs, 1),
+                                       "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "what": p.config}
     for r in reads:
         gbs = r.bytes / (r.graph_ms * 1e-3) / 1e9
         ceilings[r.name] = {"bytes": r.bytes, "us": round(r.graph_ms * 1e3, 2), "GB_s": round(gbs, 1),
@@ -693,7 +726,7 @@ def main():
             p.buffers = None
     for r in reads:
         r.buffers = None
-    probes = reads = None
+    probes = reads = rows_probes = None
     torch.cuda.synchronize()
 
     # A plain device copy of one C5 tensor (402.6 MB read + 402.6 MB
@@ -734,6 +767,8 @@ def main():
         }
         if k.name in ceilings:
             table[k.name]["frac_of_ceiling"] = round(gbs / ceilings[k.name]["GB_s"], 4)
+            if "row_probe" in ceilings[k.name]:
+                table[k.name]["frac_of_row_probe"] = round(gbs / ceilings[k.name]["row_probe"]["GB_s"], 4)
     dominant = max(kernels, key=lambda k: k.graph_ms)
     dom_avg = dominant.graph_ms
     achieved = dominant.bytes / (dom_avg * 1e-3) / 1e9

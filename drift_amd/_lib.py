@@ -78,9 +78,10 @@ SIGNATURES = {
     "drift_convert": (_I32, [_P, _P, _I64, _I32, _P]),
     "drift_read_sum_f32x4": (_I32, [_P, _I64, _P, _I32, _P]),
     "drift_stream_mix": (_I32, [_P, _I64, _P, _I64, _I32, _P]),
+    "drift_row_probe": (_I32, [_P, _I64, _I32, _P, _I64, _P, _I32, _P]),
 }
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 
 class NotBuilt(RuntimeError):

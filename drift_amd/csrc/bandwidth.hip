@@ -17,6 +17,13 @@
 // one value that is stored only if it equals a sentinel (never, for data
 // other than all ones), so no read can be dropped. Loads and stores are
 // non-temporal, as the fused kernels' are.
+//
+// row_probe moves a gather's bytes in a gather's pattern: a block per id reads
+// the whole table row the id names (row_chunks 16-byte chunks, one or two a
+// lane, all in flight together) and writes out_chunks chunks of output, each
+// lane's stores carrying the XOR of what it read. Rows drawn at random from a
+// table larger than the cache are read from scattered DRAM pages, which a
+// contiguous stream does not measure.
 #include "common.hpp"
 
 namespace drift {
@@ -77,6 +84,27 @@ __global__ void __launch_bounds__(256) stream_mix_kernel(const uint4* src, int64
   }
 }
 
+template <int L>
+__global__ void __launch_bounds__(256) row_probe_kernel(const uint4* table, int64_t rows, int row_chunks,
+                                                        const int32_t* ids, uint4* out, int out_chunks) {
+  const int64_t t = blockIdx.x;
+  const int64_t id = min(max((int64_t)ids[t], (int64_t)0), rows - 1);
+  const uint4* row = table + id * row_chunks;
+  uint4 v[L];
+#pragma unroll
+  for (int k = 0; k < L; ++k) v[k] = stream_load(row + min((int)threadIdx.x + k * 256, row_chunks - 1));
+  uint4 acc = make_uint4(0, 0, 0, 0);
+#pragma unroll
+  for (int k = 0; k < L; ++k)
+    if ((int)threadIdx.x + k * 256 < row_chunks)
+      acc = make_uint4(acc.x ^ v[k].x, acc.y ^ v[k].y, acc.z ^ v[k].z, acc.w ^ v[k].w);
+  uint4* target = out + t * out_chunks;
+  for (int j = threadIdx.x; j < out_chunks; j += 256) {
+    const u32x4 q = {acc.x ^ (uint32_t)j, acc.y, acc.z, acc.w};
+    __builtin_nontemporal_store(q, reinterpret_cast<u32x4*>(target + j));
+  }
+}
+
 }  // namespace
 }  // namespace drift
 
@@ -119,5 +147,27 @@ extern "C" int drift_stream_mix(const void* src, int64_t read_chunks, void* dst,
   else
     hipLaunchKernelGGL(stream_mix_kernel<4>, grid, dim3(256), 0, s, in, read_chunks, out, write_chunks, read_blocks,
                        write_blocks);
+  return launched(entry);
+}
+
+extern "C" int drift_row_probe(const void* table, int64_t rows, int32_t row_chunks, const int32_t* ids, int64_t count,
+                               void* out, int32_t out_chunks, void* stream) {
+  const char* entry = "drift_row_probe";
+  clear_error();
+  if (rows < 1 || row_chunks < 1 || row_chunks > 512 || count < 0 || out_chunks < 1)
+    return refuse("%s: %lld ids into %lld rows of %d chunks (1 to 512), %d chunks out each", entry, (long long)count,
+                  (long long)rows, row_chunks, out_chunks);
+  if (count == 0) return 0;
+  if (!table || !ids || !out) return refuse("%s: null table, ids or out", entry);
+  if (!aligned16(table) || !aligned16(out)) return refuse("%s: table or out is not 16-byte aligned", entry);
+  if (count > kOneShotBlocks) return refuse("%s: %lld ids", entry, (long long)count);
+  const dim3 grid((unsigned)count);
+  const hipStream_t s = (hipStream_t)stream;
+  const uint4* in = static_cast<const uint4*>(table);
+  uint4* o = static_cast<uint4*>(out);
+  if (row_chunks <= 256)
+    hipLaunchKernelGGL(row_probe_kernel<1>, grid, dim3(256), 0, s, in, rows, row_chunks, ids, o, out_chunks);
+  else
+    hipLaunchKernelGGL(row_probe_kernel<2>, grid, dim3(256), 0, s, in, rows, row_chunks, ids, o, out_chunks);
   return launched(entry);
 }

@@ -17,6 +17,15 @@
 // of 4096: 2 chunks per lane 18.4 us, 4 19.1 us, 8 (a wave per row) 20.2 us,
 // 1 27.4 us.
 //
+// What bounds it is where the rows lie, not the wait for the id: drawn at
+// random from a [151936, 4096] table (661 MB, past the 256 MB MALL) the rows
+// come from scattered DRAM pages, 19.7 us a launch (per-dispatch median),
+// where contiguous ids take 17.5 us, the contiguous 1:2 read/write stream's
+// figure. A plain copy of the same random rows with no decode (a block per
+// row, every load in flight at once) takes the same 19.7 us. Waves that
+// take two to four rows each, loading every id before any row (20.4 to
+// 26.2 us), and one-wave blocks (20.4 us) were slower.
+//
 // Codes sit at 2-byte offsets (34-byte blocks). When rows start on 4-byte
 // boundaries (an even number of blocks per row and a 4-byte aligned table) a
 // chunk's 8 codes are read as one 12-byte window from the 4-byte boundary at

@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define DRIFT_ABI_VERSION 7
+#define DRIFT_ABI_VERSION 8
 
 /* Activation kinds: src/drift/runner/ops/Activation.scala:6-20. */
 enum {
@@ -439,6 +439,15 @@ int drift_convert(const void* x, void* out, int64_t n, int32_t kind, void* strea
 int drift_read_sum_f32x4(const float* x, int64_t n4, float* partials, int32_t blocks, void* stream);
 int drift_stream_mix(const void* src, int64_t read_chunks, void* dst, int64_t write_chunks, int32_t per_thread,
                      void* stream);
+/* drift_row_probe: a gather's bytes in a gather's pattern, for its ceiling:
+ * a 256-thread block per id reads the whole row ids[t] of a table of `rows`
+ * rows of row_chunks (1 to 512) 16-byte chunks (ids clamped into the
+ * table), and writes out_chunks chunks to row t of out, thread i's chunks
+ * holding the XOR of the row chunks i and i + 256 it read (the first word
+ * also XORed with the chunk index). table and out 16-byte aligned. No
+ * counterpart in the reference. */
+int drift_row_probe(const void* table, int64_t rows, int32_t row_chunks, const int32_t* ids, int64_t count, void* out,
+                    int32_t out_chunks, void* stream);
 
 #ifdef __cplusplus
 }

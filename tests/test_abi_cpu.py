@@ -23,7 +23,7 @@ def test_header_and_library_agree(lib):
 
 
 def test_version_and_error_text(lib):
-    assert lib.drift_abi_version() == _lib.ABI_VERSION == 7
+    assert lib.drift_abi_version() == _lib.ABI_VERSION == 8
     assert lib.drift_error_string(0).decode().lower().startswith("no error")
     assert lib.drift_error_string(1)
 
@@ -161,3 +161,7 @@ def test_probes_refuse_bad_geometry(lib):
     assert "at least one written" in refused(lib, "drift_stream_mix", p, 10, p, 0, 1, NULL)
     assert "3 a lane" in refused(lib, "drift_stream_mix", p, 10, p, 10, 3, NULL)
     assert "null" in refused(lib, "drift_stream_mix", NULL, 10, p, 10, 1, NULL)
+    assert "rows of 513 chunks (1 to 512)" in refused(lib, "drift_row_probe", p, 10, 513, p, 4, p, 8, NULL)
+    assert "0 rows" in refused(lib, "drift_row_probe", p, 0, 16, p, 4, p, 8, NULL)
+    assert "null" in refused(lib, "drift_row_probe", p, 10, 16, NULL, 4, p, 8, NULL)
+    assert "not 16-byte aligned" in refused(lib, "drift_row_probe", p, 10, 16, p, 4, ctypes.c_void_p(8), 8, NULL)

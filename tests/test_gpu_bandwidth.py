@@ -45,3 +45,33 @@ def test_stream_mix_reads_all_and_writes_all(reads, writes, per):
     assert np.array_equal(got[:, 1], (i >> np.uint64(32)).astype(np.uint32))
     assert np.array_equal(got[:, 2], ((i // 256) % per).astype(np.uint32))
     assert np.all(got[:, 3] == 0x5EED)
+
+
+@pytest.mark.parametrize("rows,row_chunks,count,out_chunks", [(5, 1, 3, 1), (40, 272, 17, 512), (9, 256, 8, 300),
+                                                              (300, 512, 64, 1000), (3, 100, 1, 3)])
+def test_row_probe_writes_what_each_row_holds(rows, row_chunks, count, out_chunks):
+    # thread i of the block for id t XORs row chunks i and i + 256 (those in
+    # the row) and stores that, its first word XORed with the chunk index,
+    # into every chunk j = i (mod 256) of out row t; ids outside the table
+    # are clamped into it
+    step(f"row_probe {count} ids into {rows} rows of {row_chunks} chunks, {out_chunks} out")
+    rng = np.random.default_rng(rows + row_chunks)
+    table = rng.integers(0, 2**32, (rows, row_chunks, 4), dtype=np.uint64).astype(np.uint32)
+    ids = rng.integers(-2, rows + 2, count).astype(np.int32)
+    dt = torch.from_numpy(table.view(np.int32)).to(DEV)
+    di = torch.from_numpy(ids).to(DEV)
+    out = torch.zeros((count, out_chunks, 4), dtype=torch.int32, device=DEV)
+    _lib.call("drift_row_probe", ctypes.c_void_p(dt.data_ptr()), rows, row_chunks, ctypes.c_void_p(di.data_ptr()),
+              count, ctypes.c_void_p(out.data_ptr()), out_chunks, None)
+    got = out.cpu().numpy().view(np.uint32)
+    want = np.zeros((count, out_chunks, 4), dtype=np.uint32)
+    for t, id_ in enumerate(np.clip(ids, 0, rows - 1)):
+        folded = np.zeros((256, 4), dtype=np.uint32)
+        for i in range(256):
+            for k in (i, i + 256):
+                if k < row_chunks:
+                    folded[i] ^= table[id_, k]
+        j = np.arange(out_chunks)
+        want[t] = folded[j % 256]
+        want[t, :, 0] ^= j.astype(np.uint32)
+    assert np.array_equal(got, want)
