@@ -403,6 +403,64 @@ __global__ void __launch_bounds__(256) decode_staged(const uint8_t* table, const
   }
 }
 
+// The 256-value formats a run of 8 blocks at a time, for rows of whole runs
+// on 16-byte boundaries: a one-wave block copies the run's bytes (8 x 136 to
+// 8 x 210, a multiple of 16) into LDS with two 16-byte loads a lane, all in
+// flight together, then each lane decodes 4 chunks (chunk k * 64 + lane of
+// the run's 256) from there, so each store instruction writes 64
+// consecutive 16-byte pieces. decode_staged's 4-byte copies of one block
+// per half wave keep too few bytes in flight to cover HBM's latency.
+constexpr int kRunBlocks = 8;
+
+template <typename F>
+constexpr int run_pieces() {
+  return kRunBlocks * F::kBytes / 16;
+}
+
+template <typename T, typename F>
+__global__ void __launch_bounds__(kWave) decode_runs(const uint8_t* table, const int32_t* ids, T* out, int64_t count,
+                                                     int64_t vocab, int cols, int64_t row_bytes, int32_t* bad_id) {
+  static_assert(F::kValues == 256 && (kRunBlocks * F::kBytes) % 16 == 0, "runs of whole 16-byte pieces");
+  constexpr int kPieces = run_pieces<F>();
+  constexpr int kLoads = (kPieces + kWave - 1) / kWave;
+  constexpr int kFieldAlign = F::kBytes % 8 == 0 ? 8 : 2;  // where the run puts each block
+  __shared__ __align__(16) uint8_t staged[kPieces * 16];
+  __shared__ float lut[16];
+  const int lane = (int)threadIdx.x;
+  if constexpr (F::kLut != 0) {
+    if (lane < 16) lut[lane] = lut_entry(F::kLut, lane);
+  }
+  const int runs_per_row = cols / (256 * kRunBlocks);
+  const int64_t run = blockIdx.x;
+  const int64_t t = run / runs_per_row;
+  const int r = (int)(run - t * runs_per_row);
+  const int64_t id = ids ? ids[t] : t;
+  const bool bad = id < 0 || id >= vocab;
+  const uint4* src =
+      reinterpret_cast<const uint4*>(table + (bad ? 0 : id) * row_bytes + (int64_t)r * kRunBlocks * F::kBytes);
+  uint4 piece[kLoads];
+#pragma unroll
+  for (int k = 0; k < kLoads; ++k) piece[k] = stream_load(src + min(lane + k * kWave, kPieces - 1));
+#pragma unroll
+  for (int k = 0; k < kLoads; ++k)
+    if (lane + k * kWave < kPieces) reinterpret_cast<uint4*>(staged)[lane + k * kWave] = piece[k];
+  wave_sync();
+  if (bad && bad_id && lane == 0) *bad_id = 1;
+  T* target = out + t * cols + (int64_t)r * kRunBlocks * 256;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int chunk = k * kWave + lane;
+    float v[8];
+    if (bad) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = 0.0f;
+    } else {
+      F::template decode<kFieldAlign>(staged + (chunk >> 5) * F::kBytes, chunk & 31, v, lut);
+    }
+    store_chunk<T>(target + chunk * 8, v);
+  }
+}
+
 // ---------------------------------------------------------------- launch layer
 
 // A format's block and alignment, for the checks: values, bytes, alignment.
@@ -478,6 +536,12 @@ int decode_launch(const char* entry, const void* table, int32_t format, const in
 #define DRIFT_DECODE(CODE, F)                                                                                     \
   case CODE:                                                                                                     \
     if constexpr (F::kValues == 256) {                                                                           \
+      const int64_t runs = count * (cols / (256 * kRunBlocks));                                                  \
+      if (vocab > 0 && cols % (256 * kRunBlocks) == 0 && aligned16(table) && runs <= kOneShotBlocks) {           \
+        hipLaunchKernelGGL((decode_runs<T, F>), dim3((unsigned)runs), dim3(kWave), 0, s, bytes, ids, out, count,  \
+                           vocab, cols, row_bytes, bad_id);                                                      \
+        break;                                                                                                   \
+      }                                                                                                          \
       if (vocab > 0) {                                                                                           \
         const dim3 staged(grid_for(count * (cols / 256), 8, kOneShotBlocks));                                    \
         hipLaunchKernelGGL((decode_staged<T, F>), staged, dim3(256), 0, s, bytes, ids, out, count, vocab, cols,    \

@@ -69,6 +69,61 @@ def test_dequantize_every_storage_type(hip, name, out_type):
     assert_bits(expected, host_bits(out), what=f"{name} dequantize {out_type}")
 
 
+RUN_FORMATS = [n for n in NAMES if d.STORAGE_TYPES[n].values == 256]
+
+
+@pytest.mark.parametrize("name", RUN_FORMATS)
+@pytest.mark.parametrize("cols", [2048, 6144])
+def test_rows_of_whole_runs(hip, name, cols):
+    # rows of whole runs of 8 blocks, the table on a 16-byte boundary: the
+    # run decoder, for the gather (with ids outside the table: zero rows and
+    # the flag) and the whole-table decode
+    vocab = 19
+    raw, table = table_of(name, vocab, cols, 41 + cols)
+    assert table.data.data_ptr() % 16 == 0
+    ids = np.random.default_rng(cols).integers(0, vocab, 23).astype(np.int32)
+    ids[:2] = [vocab - 1, 0]
+    bad_ids = ids.copy()
+    bad_ids[[5, 11]] = [-1, vocab]
+    step(f"embedding {name} rows of {cols}, ids outside the table")
+    want = o.embedding(name, raw, vocab, cols, ids)
+    want[[5, 11]] = 0.0
+    bad = torch.zeros(1, dtype=torch.int32, device=DEV)
+    out = torch.empty((ids.size, cols), dtype=torch.float32, device=DEV)
+    hip.embedding(table, dev_i32(bad_ids), out, bad)
+    assert_bits(want.view(np.uint32), host_f32(out).view(np.uint32), what=f"{name} f32 rows of {cols}")
+    assert int(bad.item()) == 1
+    out = torch.empty((ids.size, cols), dtype=torch.bfloat16, device=DEV)
+    hip.embedding(table, dev_i32(ids), out)
+    want = o.embedding(name, raw, vocab, cols, ids)
+    assert_bits(o.to_bf16(want), host_bits(out), what=f"{name} bf16 rows of {cols}")
+    step(f"dequantize {name} [{vocab}, {cols}] to bf16 and f16")
+    whole = o.embedding(name, raw, vocab, cols, np.arange(vocab, dtype=np.int32))
+    for dtype, expected in ((torch.bfloat16, o.to_bf16(whole)), (torch.float16, whole.astype(np.float16).view(np.uint16))):
+        out = torch.empty((vocab, cols), dtype=dtype, device=DEV)
+        hip.dequantize(table, out)
+        assert_bits(expected, host_bits(out), what=f"{name} dequantize {dtype} rows of {cols}")
+
+
+@pytest.mark.parametrize("name", RUN_FORMATS)
+def test_runs_off_a_16_byte_boundary(hip, name):
+    # the same rows from a table 8 bytes past a 16-byte boundary: the
+    # one-block-a-half-wave decoder, with the same result
+    vocab, cols = 7, 2048
+    raw, _ = table_of(name, vocab, cols, 77)
+    t = d.STORAGE_TYPES[name]
+    flat = torch.zeros(raw.size + 8, dtype=torch.uint8, device=DEV)
+    flat[8:] = torch.from_numpy(np.ascontiguousarray(raw).reshape(-1)).to(DEV)
+    table = d.StoredTable(flat[8:].view(vocab, t.rowBytes(cols)), t, cols)
+    assert table.data.data_ptr() % 16 == 8
+    ids = np.array([3, 0, 6, 3], np.int32)
+    step(f"embedding {name} rows of {cols} from a table 8 bytes off a 16-byte boundary")
+    out = torch.empty((ids.size, cols), dtype=torch.float32, device=DEV)
+    hip.embedding(table, dev_i32(ids), out)
+    want = o.embedding(name, raw, vocab, cols, ids)
+    assert_bits(want.view(np.uint32), host_f32(out).view(np.uint32), what=f"{name} f32 off 16")
+
+
 @pytest.mark.parametrize("name", ["Q4_K", "IQ4_NL", "Q4_0_ROCMFP4_FAST"])
 def test_ids_outside_the_table_give_zero_rows(hip, name):
     values = d.STORAGE_TYPES[name].values
