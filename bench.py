@@ -665,6 +665,9 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=24.0, help="seconds of CPU reference work, about")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="", help="comma-separated kernel names to run (profiling)")
+    ap.add_argument("--no-host", action="store_true",
+                    help="skip the host cost per call (a child process that launches kernels of its own: profilers "
+                         "tracing this process would trace it too)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this path runs on one GPU; --gpus {args.gpus} is not supported "
@@ -749,7 +752,7 @@ def main():
     copy_gbs = 2 * copy_elems * 2 / (copy_ms * 1e-3) / 1e9
     del src, dsts
 
-    host = None if args.only else host_call_cost()
+    host = None if args.only or args.no_host else host_call_cost()
 
     if not args.no_cpu:
         cpu_baseline(kernels, args.cpu_budget)
