@@ -112,7 +112,7 @@ REFERENCE_ROPE = d.Rope(1e7, 64, d.RopeLayout.Neox, d.RopeSections.Interleaved(1
 QWEN3_ROPE = d.Rope(1e6, 128, d.RopeLayout.Neox, d.RopeSections.Single())
 
 
-def run_attention_inputs(hip, dtype, t, heads, kv, dim, rope, start, table, pages, gated, seed):
+def run_attention_inputs(hip, dtype, t, heads, kv, dim, rope, start, table, pages, gated, seed, offset=0.0):
     rng = np.random.default_rng(seed)
     width = 2 * dim if gated else dim
     qg = (2 * rng.standard_normal((t, heads, width))).astype(np.float32)
@@ -124,7 +124,7 @@ def run_attention_inputs(hip, dtype, t, heads, kv, dim, rope, start, table, page
     positions = np.array([start + i % t + i // t for i in range(count * t)], np.int32)
     positions = positions.reshape(count, t) if count > 1 else positions
     c, keys0, values0 = cache(pages, kv, dim, seed + 1)
-    norms = d.QueryKeyNorms(dev_f32(qw), dev_f32(kw), 1e-6, 0.0, rope)
+    norms = d.QueryKeyNorms(dev_f32(qw), dev_f32(kw), 1e-6, offset, rope)
     bf = dtype == "bf16"
     if bf:
         qgb, kb, vb = bf16_input(qg), bf16_input(k), bf16_input(v)
@@ -146,7 +146,7 @@ def run_attention_inputs(hip, dtype, t, heads, kv, dim, rope, start, table, page
         hip.queryKeyNormRopeCache(inputs[0], inputs[1], inputs[2], norms, dev_i32(positions), c, dev_i32(table),
                                   start, rotated, bad)
     want_q, want_gate, want_k, want_v = o.attention_inputs(
-        qg, k, v, qw, kw, 1e-6, 0.0, positions, rope.theta, rope.rotaryDimensions, keys0, values0, table, PAGE,
+        qg, k, v, qw, kw, 1e-6, offset, positions, rope.theta, rope.rotaryDimensions, keys0, values0, table, PAGE,
         start, int(rope.layout), rope.sections.code, rope.sections.sizes, gated)
     what = f"{dtype} {t} tokens"
     if bf:
@@ -179,6 +179,18 @@ def test_attention_inputs_qwen3_shape(hip, dtype, t, gated):
     pages = -(-(start + t) // PAGE) + 2
     table = np.random.default_rng(t).permutation(pages).astype(np.int32)
     run_attention_inputs(hip, dtype, t, 32, 8, 128, QWEN3_ROPE, start, table, pages, gated, 90 + t)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("gated", [True, False])
+def test_attention_inputs_with_a_weight_offset(hip, dtype, gated):
+    # norms of (weight + 1), as a Gemma-style model passes them: the body
+    # that adds the offset
+    t, start = 19, 3
+    step(f"attentionInputs {dtype} Qwen3 heads with a weight offset of 1, gated {gated}")
+    pages = -(-(start + t) // PAGE) + 1
+    table = np.random.default_rng(7).permutation(pages).astype(np.int32)
+    run_attention_inputs(hip, dtype, t, 32, 8, 128, QWEN3_ROPE, start, table, pages, gated, 150, offset=1.0)
 
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])

@@ -207,3 +207,42 @@ def test_query_key_norm_rope(hip, case, dtype):
         wq, wk = o.qk_norm_rope_bf16(qb, kb, *args)
         assert_bf16(wq, host_bits(qd), what="queries bf16")
         assert_bf16(wk, host_bits(kd), what="keys bf16")
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("far,offset", [(True, 0.0), (False, 1.0), (True, 1.0)])
+def test_query_key_norm_rope_far_positions_and_weight_offsets(hip, dtype, far, offset):
+    # positions whose angles pass 2^20 (pair 0 turns by the position itself)
+    # take the library's sincos instead of the reduced one; a weight offset
+    # (norms of 1 + w) takes the body that adds it
+    tokens, heads, kv, dim = 24, 8, 2, 128
+    rope = d.Rope(1e6, 128, d.RopeLayout.Neox)
+    q = gaussian(21, (tokens, heads, dim))
+    k = gaussian(22, (tokens, kv, dim))
+    qw = (0.1 * gaussian(23, dim)).astype(np.float32)
+    kw = (0.1 * gaussian(24, dim)).astype(np.float32)
+    if far:
+        p = np.array([0, 1, 1048575, 1048576, 1048577, 2000003, 3 << 20, 16777215, 12345678, 7, 999999, 1 << 23,
+                      5000000, 65536, 4095, 2097151, 2097152, 8388607, 9000001, 31, 131071, 1 << 22, 123456, 6000000],
+                     np.int32)
+    else:
+        p = ((np.arange(tokens) * 131) % 4096).astype(np.int32)
+    args = (qw, kw, p, 1e-6, offset, rope.theta, rope.rotaryDimensions, int(rope.layout), rope.sections.code,
+            rope.sections.sizes)
+    norms = d.QueryKeyNorms(dev_f32(qw), dev_f32(kw), 1e-6, offset, rope)
+    step(f"queryKeyNormRope {dtype}, positions {'past 2^20' if far else 'below 4096'}, weight offset {offset}")
+    if dtype == "f32":
+        rq = torch.empty(q.shape, dtype=torch.float32, device=DEV)
+        rk = torch.empty(k.shape, dtype=torch.float32, device=DEV)
+        hip.queryKeyNormRope(dev_f32(q), dev_f32(k), norms, dev_i32(p), rq, rk)
+        wq, wk = o.qk_norm_rope(q, k, *args)
+        assert_f32(wq, host_f32(rq), what="queries")
+        assert_f32(wk, host_f32(rk), what="keys")
+    else:
+        qb, kb = bf16_input(q), bf16_input(k)
+        rq = torch.empty(q.shape, dtype=torch.bfloat16, device=DEV)
+        rk = torch.empty(k.shape, dtype=torch.bfloat16, device=DEV)
+        hip.queryKeyNormRope(dev_bf16(qb), dev_bf16(kb), norms, dev_i32(p), rq, rk)
+        wq, wk = o.qk_norm_rope_bf16(qb, kb, *args)
+        assert_bf16(wq, host_bits(rq), what="queries bf16")
+        assert_bf16(wk, host_bits(rk), what="keys bf16")
