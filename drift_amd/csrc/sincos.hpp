@@ -40,21 +40,24 @@ __host__ __device__ inline bool sincos_reduced(float angle, double* s, double* c
   r = fma(-k, kPio2Mid, r);
   r = fma(-k, kPio2Lo, r);
   const double z = r * r;
+  // Horner steps as fma: one rounding a step instead of two, and half the
+  // double-precision instructions (the kernels build with contraction off)
   // __kernel_sin(r, 0, 0): r + r z (S1 + z (S2 + z (S3 + z (S4 + z (S5 + z S6)))))
   const double S1 = -1.66666666666666324348e-01, S2 = 8.33333333332248946124e-03,
                S3 = -1.98412698298579493134e-04, S4 = 2.75573137070700676789e-06,
                S5 = -2.50507602534068634195e-08, S6 = 1.58969099521155010221e-10;
-  const double ps = S2 + z * (S3 + z * (S4 + z * (S5 + z * S6)));
-  const double sn = r + r * z * (S1 + z * ps);
+  const double ps = fma(z, fma(z, fma(z, fma(z, S6, S5), S4), S3), S2);
+  const double sn = fma(r * z, fma(z, ps, S1), r);
   // __kernel_cos(r, 0): w + (((1 - w) - z/2) + z^2 (C1 + ...)), w = 1 - z/2
   const double C1 = 4.16666666666666019037e-02, C2 = -1.38888888888741095749e-03,
                C3 = 2.48015872894767294178e-05, C4 = -2.75573143513906633035e-07,
                C5 = 2.08757232129817482790e-09, C6 = -1.13596475577881948265e-11;
-  const double pc = z * (C1 + z * (C2 + z * (C3 + z * (C4 + z * (C5 + z * C6)))));
+  const double pc = fma(z, fma(z, fma(z, fma(z, fma(z, C6, C5), C4), C3), C2), C1);
   const double hz = 0.5 * z, w = 1.0 - hz;
-  const double cs = w + (((1.0 - w) - hz) + z * pc);
-  // quadrant k mod 4: sin, cos of k pi/2 + r
-  const int q = (int)((long long)k & 3);
+  const double cs = w + fma(z * z, pc, (1.0 - w) - hz);
+  // quadrant k mod 4: sin, cos of k pi/2 + r (|k| < 2^20: an int holds it,
+  // and its two's complement low bits are k mod 4 for negative k too)
+  const int q = (int)k & 3;
   const double s0 = (q & 1) ? cs : sn, c0 = (q & 1) ? sn : cs;
   *s = (q & 2) ? -s0 : s0;
   *c = ((q + 1) & 2) ? -c0 : c0;

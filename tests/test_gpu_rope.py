@@ -175,6 +175,9 @@ QK_CASES = [
     (9, 4, 2, 256, d.Rope(1e7, 64, d.RopeLayout.Neox)),                      # partial rotary: generic kernel
     (9, 3, 1, 80, d.Rope(1e4, 80, d.RopeLayout.Interleaved)),                # 80 values: generic kernel
     (5, 6, 0, 128, d.Rope(1e6, 128, d.RopeLayout.Neox)),                     # no key heads
+    # two groups of heads a wave, the key waves' second group part-filled or empty
+    (19, 16, 12, 128, d.Rope(1e6, 128, d.RopeLayout.Neox)),
+    (11, 32, 4, 64, d.Rope(1e4, 64, d.RopeLayout.Interleaved)),
 ]
 
 
@@ -207,6 +210,43 @@ def test_query_key_norm_rope(hip, case, dtype):
         wq, wk = o.qk_norm_rope_bf16(qb, kb, *args)
         assert_bf16(wq, host_bits(qd), what="queries bf16")
         assert_bf16(wk, host_bits(kd), what="keys bf16")
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_query_key_norm_rope_zero_epsilon(hip, dtype):
+    # epsilon 0 takes the inverse square root that handles a zero mean: a
+    # zero head's 1 / sqrt(0) is infinite and 0 times it NaN, as in the
+    # reference's double arithmetic; the other heads are normed as usual
+    tokens, heads, kv, dim = 6, 16, 4, 128
+    rope = d.Rope(1e6, 128, d.RopeLayout.Neox)
+    q = gaussian(31, (tokens, heads, dim))
+    k = gaussian(32, (tokens, kv, dim))
+    q[1, 3] = 0.0
+    q[4, 15] = 0.0
+    k[2, 1] = 0.0
+    qw = (1 + 0.1 * gaussian(33, dim)).astype(np.float32)
+    kw = (1 + 0.1 * gaussian(34, dim)).astype(np.float32)
+    p = ((np.arange(tokens) * 131) % 4096).astype(np.int32)
+    args = (qw, kw, p, 0.0, 0.0, rope.theta, rope.rotaryDimensions, int(rope.layout), rope.sections.code,
+            rope.sections.sizes)
+    norms = d.QueryKeyNorms(dev_f32(qw), dev_f32(kw), 0.0, 0.0, rope)
+    step(f"queryKeyNormRope {dtype}, epsilon 0, zero heads")
+    if dtype == "f32":
+        rq = torch.empty(q.shape, dtype=torch.float32, device=DEV)
+        rk = torch.empty(k.shape, dtype=torch.float32, device=DEV)
+        hip.queryKeyNormRope(dev_f32(q), dev_f32(k), norms, dev_i32(p), rq, rk)
+        wq, wk = o.qk_norm_rope(q, k, *args)
+        assert np.isnan(wq[1, 3]).all() and np.isnan(wk[2, 1]).all()
+        assert_f32(wq, host_f32(rq), what="queries")
+        assert_f32(wk, host_f32(rk), what="keys")
+    else:
+        qb, kb = bf16_input(q), bf16_input(k)
+        rq = torch.empty(q.shape, dtype=torch.bfloat16, device=DEV)
+        rk = torch.empty(k.shape, dtype=torch.bfloat16, device=DEV)
+        hip.queryKeyNormRope(dev_bf16(qb), dev_bf16(kb), norms, dev_i32(p), rq, rk)
+        wq, wk = o.qk_norm_rope_bf16(qb, kb, *args)
+        assert_bf16(wq, host_bits(rq), what="queries bf16")
+        assert_bf16(wk, host_bits(rk), what="keys bf16")
 
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
