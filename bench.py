@@ -17,8 +17,9 @@ Inputs are synthetic (seeded device generators) and resident in HBM. Each
 kernel rotates through buffer sets totalling more than 512 MB, so the 256 MB
 Infinity Cache cannot hold what the next launch reads.
 
-The timed region replays, kernel by kernel, a HIP graph holding that
-kernel's K launches (K launches of one kernel, then K of the next), so no
+The timed region replays, kernel by kernel (largest first, so that no short
+kernel is timed while the clocks rise after the decode kernels' idle gaps),
+a HIP graph holding that kernel's K launches (K of one, then K of the next), so no
 kernel reads what the kernel before it left in the Infinity Cache or pays
 for the dirty lines it left there, and no host call sits between launches.
 Every call is checked by the Ops layer beforehand; the graphs capture the
@@ -33,7 +34,11 @@ peak, fraction of its ceiling and rows/s; `ceilings` is the streaming probe
 (drift_stream_mix) moving each long kernel's bytes in its read:write mix,
 for the gather also its own pattern with no decode (drift_row_probe: the
 rows its ids name read, its output written; `frac_of_row_probe`), and the
-reference's streaming read (drift_read_sum_f32x4) over 1 GiB;
+reference's streaming read (drift_read_sum_f32x4) over 1 GiB. A probe's
+launches fall into two or three durations by clock and memory state, so
+each kernel is also replayed in alternation with its best probe
+(`ceilings[k]["matched"]`, and `frac_of_probe_matched`: the median replays'
+ratio under the same conditions);
 `roofline` is the dominant kernel's; `cpu_baseline` is the CPU reference
 arithmetic (the oracle) timed on a bounded sample of the same work on this
 host's cores, scaled to the whole step.
@@ -47,6 +52,7 @@ import faulthandler
 import json
 import math
 import os
+import statistics
 import sys
 import time
 import subprocess
@@ -63,6 +69,7 @@ from drift_amd import _lib  # noqa: E402
 from drift_amd import ops as d  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
+MATCHED_ROUNDS = 7  # alternations of each kernel with its probe
 MALL_BYTES = 512 << 20
 DEV = "cuda:0"
 
@@ -82,6 +89,7 @@ class Kernel:
         self.cpu = None  # (sample description, seconds for the sample, fraction of a call the sample is)
         self.cpu_all = None  # (threads, seconds for the same sample split across them)
         self.graph_ms = None  # average launch, replayed from a captured graph
+        self.matched_ms = None  # the same, in alternation with its probe (median replay)
         self.eager_ms = None  # average launch, each made from Python through ctypes
         self.ceiling = None  # the stream probe at this kernel's bytes and read/write mix
 
@@ -624,6 +632,43 @@ def time_graphs(kernels, steps: int, warmup: int) -> float:
     return wall
 
 
+def time_matched(groups, steps: int, rounds: int) -> None:
+    """Each group (a kernel, then its probes) replayed from captured graphs in
+    turn, `rounds` times, one event pair around each replay: a kernel and its
+    probes see the same clocks and memory state, which change from launch to
+    launch (a probe's launches at one size fall into two or three
+    durations). Sets `matched_ms` on each to its median replay's average
+    launch."""
+    stream = torch.cuda.current_stream()
+    here = ctypes.c_void_p(stream.cuda_stream)
+    for group in groups:
+        graphs = []
+        for k in group:
+            for i in range(2):
+                k.fire(i, here)
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                captured = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+                for i in range(steps):
+                    k.fire(i, captured)
+            graphs.append(g)
+        for g in graphs:
+            g.replay()
+        torch.cuda.synchronize()
+        events = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in group]
+                  for _ in range(rounds)]
+        for r in range(rounds):
+            for g, (start, end) in zip(graphs, events[r]):
+                start.record(stream)
+                g.replay()
+                end.record(stream)
+        torch.cuda.synchronize()
+        for j, k in enumerate(group):
+            k.matched_ms = statistics.median(events[r][j][0].elapsed_time(events[r][j][1]) for r in range(rounds)) / steps
+        del graphs
+
+
 def time_eager(kernels, steps: int) -> None:
     """The same launches made one by one from Python through ctypes, as a
     caller without graphs makes them: for launches shorter than the host's
@@ -701,8 +746,12 @@ def main():
 
     # kernels: graph replays (kernel time) and Python-driven launches (what a
     # caller without graphs sees); the probes: graph replays
-    wall = time_graphs(kernels, args.steps, args.warmup)
-    time_eager(kernels, args.steps)
+    # largest first: after an idle gap the clocks take some milliseconds to
+    # rise, and a 17 us kernel timed right after the decode kernels' short
+    # launches ran 25% slower than the same kernel after a long one
+    largest_first = sorted(kernels, key=lambda k: k.bytes, reverse=True)
+    wall = time_graphs(largest_first, args.steps, args.warmup)
+    time_eager(largest_first, args.steps)
     time_graphs([p for group in probes.values() for p in group] + list(rows_probes.values()) + reads, args.steps,
                 args.warmup)
     ceilings = {}
@@ -716,6 +765,20 @@ def main():
                             "chunks_a_lane": best.per_lane, "us": round(best.graph_ms * 1e3, 2),
                             "GB_s": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
                             "us_by_chunks_a_lane": {p.per_lane: round(p.graph_ms * 1e3, 2) for p in probes[k.name]}}
+    # each kernel against its best probe (and the gather against its row
+    # probe) under the same conditions, in alternation
+    groups = [[k, k.ceiling] + ([rows_probes[k.name]] if k.name in rows_probes else []) for k in kernels
+              if k.ceiling is not None]
+    time_matched(groups, args.steps, MATCHED_ROUNDS)
+    for group in groups:
+        k, probe = group[0], group[1]
+        matched = {"rounds": MATCHED_ROUNDS, "us": round(k.matched_ms * 1e3, 2),
+                   "probe_us": round(probe.matched_ms * 1e3, 2),
+                   "frac_of_probe": round(probe.matched_ms / k.matched_ms, 4)}
+        if len(group) > 2:
+            matched["row_probe_us"] = round(group[2].matched_ms * 1e3, 2)
+            matched["frac_of_row_probe"] = round(group[2].matched_ms / k.matched_ms, 4)
+        ceilings[k.name]["matched"] = matched
     for name, p in rows_probes.items():
         gbs = p.bytes / (p.graph_ms * 1e-3) / 1e9
         ceilings[name]["row_probe"] = {"us": round(p.graph_ms * 1e3, 2), "GB_s": round(gbs, 1),
@@ -770,6 +833,7 @@ def main():
         }
         if k.name in ceilings:
             table[k.name]["frac_of_ceiling"] = round(gbs / ceilings[k.name]["GB_s"], 4)
+            table[k.name]["frac_of_probe_matched"] = ceilings[k.name]["matched"]["frac_of_probe"]
             if "row_probe" in ceilings[k.name]:
                 table[k.name]["frac_of_row_probe"] = round(gbs / ceilings[k.name]["row_probe"]["GB_s"], 4)
     dominant = max(kernels, key=lambda k: k.graph_ms)
