@@ -151,6 +151,27 @@ __device__ __forceinline__ void keep_nans(const uint32_t (&w)[8], const uint32_t
     if ((bad[j / 16] >> nibble_code(w, j)) & 1u) v[j] = __builtin_nanf("");
 }
 
+// A lane's 64 4-bit values by a table, where the relative scales cover 64
+// columns or more: the lane's 64 values then share one relative scale and
+// one row scale, so a value is the lane's own function of its code. The lane
+// makes its 16 (the level as above, a NaN product kept as NaN, times the
+// scale) once and reads each value's from the wave's LDS, at word code * 64 +
+// lane: the 64 lanes of a read fall on distinct banks, and a lane reads only
+// what it wrote. Per value an LDS read replaces the multiply, rounding, clamp
+// and multiply; the NaN cases need no pass of their own.
+__device__ __forceinline__ void decode_by_table(const uint32_t (&w)[8], const float* codebook, float rel, float scale,
+                                                float* table, float (&v)[kLaneValues]) {
+  const int lane = (int)threadIdx.x % kWave;
+#pragma unroll
+  for (int c = 0; c < 16; ++c) {
+    const float x = codebook[c] * rel;
+    const float level = x != x ? x : fminf(fmaxf(__builtin_rintf(x), -127.0f), 127.0f);
+    table[c * kWave + lane] = level * scale;
+  }
+#pragma unroll
+  for (int j = 0; j < kLaneValues; ++j) v[j] = table[nibble_code(w, j) * kWave + lane];
+}
+
 // What decodes a rotated weight (ops/ConvRotParts.scala): scales F32, one a
 // row or one for all; with a codebook, the 4-bit levels' codebook (F32
 // [16]), relative scales (fp8 [rows, cols / group_size]) and group_size.
@@ -166,9 +187,12 @@ struct Parts {
 // Rows ids[t] (row t with no ids) of a rotated weight [rows, cols] into out
 // [count, cols]; T float (the BF16 value widened, as the reference gathers)
 // or uint16_t (BF16). An id outside [0, rows) gets zeros and sets *bad_id.
-template <typename T, bool FOUR_BIT, bool ALIGNED>
+// TABLE (4-bit, relative scales a group of 64 columns or more): the values
+// by decode_by_table.
+template <typename T, bool FOUR_BIT, bool ALIGNED, bool TABLE = false>
 __global__ void __launch_bounds__(kBlockWaves * kWave)
     rotated_rows(Parts parts, const int32_t* ids, T* out, int64_t count, int64_t rows, int cols, int32_t* bad_id) {
+  static_assert(!TABLE || FOUR_BIT, "the table is the 4-bit codes'");
   __shared__ float4 trade[kBlockWaves][kWaveGroups * 16];  // 4 KiB a wave
   const int lane = (int)threadIdx.x % kWave, wave = (int)threadIdx.x / kWave;
   const int g = lane >> 2, q = lane & 3;  // group in the wave, quarter in the group
@@ -192,6 +216,12 @@ __global__ void __launch_bounds__(kBlockWaves * kWave)
     load_codes<64, ALIGNED>(parts.codes + row * cols + first, w);
 #pragma unroll
     for (int j = 0; j < kLaneValues; ++j) v[j] = (float)(int8_t)(w[j / 4] >> (8 * (j % 4))) * scale;
+  } else if constexpr (TABLE) {
+    uint32_t w[8];
+    load_codes<32, ALIGNED>(parts.codes + row * (cols / 2) + first / 2, w);
+    const float rel = e4m3(parts.relative[row * (cols / parts.group_size) + first / parts.group_size]);
+    decode_by_table(w, parts.codebook, rel, scale, reinterpret_cast<float*>(trade[wave]), v);
+    wave_sync();  // the table's reads are done before the trade writes over it
   } else {
     // ops/CpuBase.scala:50-66: the low nibble the even column; level =
     // clamp(rint(codebook(code) * relative), -127, 127), a NaN kept (Java's
@@ -324,7 +354,14 @@ int rotated_launch(const char* entry, const Parts& parts, const int32_t* ids, T*
   const bool aligned = aligned16(parts.codes);
   const hipStream_t s = (hipStream_t)stream;
   const dim3 grid((unsigned)blocks), block(kBlockWaves * kWave);
-  if (four_bit) {
+  if (four_bit && parts.group_size % 64 == 0) {
+    if (aligned)
+      hipLaunchKernelGGL((rotated_rows<T, true, true, true>), grid, block, 0, s, parts, ids, out, count, rows, cols,
+                         bad_id);
+    else
+      hipLaunchKernelGGL((rotated_rows<T, true, false, true>), grid, block, 0, s, parts, ids, out, count, rows, cols,
+                         bad_id);
+  } else if (four_bit) {
     if (aligned)
       hipLaunchKernelGGL((rotated_rows<T, true, true>), grid, block, 0, s, parts, ids, out, count, rows, cols, bad_id);
     else
