@@ -281,28 +281,6 @@ __device__ __forceinline__ void cache_values_tile(const Extras<T>& e, int64_t to
   }
 }
 
-// 1 / sqrt(m) by the hardware's reciprocal square root and two Newton steps
-// (within a double ulp or two of the correctly rounded quotient of the
-// correctly rounded root, which moves an F32 result only where it lies that
-// close to a rounding boundary). Without a branch: a subnormal m is scaled
-// into range first (2^256 m, the result times 2^128), and 0 and infinity give
-// the division's own infinity and zero; NaN stays NaN. With NORMAL the caller
-// knows m is at least 2^-1000 or not a number (a positive epsilon is added to
-// it), and the scaling and the zero case are left out.
-template <bool NORMAL = false>
-__device__ __forceinline__ double inverse_sqrt(double m) {
-  const bool tiny = !NORMAL && m < 0x1p-1000;
-  const double ms = tiny ? m * 0x1p256 : m;
-  double y = __builtin_amdgcn_rsq(ms);
-  y = y * fma(-0.5 * ms * y, y, 1.5);
-  y = y * fma(-0.5 * ms * y, y, 1.5);
-  if constexpr (!NORMAL) {
-    y = tiny ? y * 0x1p128 : y;
-    y = m == 0.0 ? __builtin_huge_val() : y;
-  }
-  return m == __builtin_huge_val() ? 0.0 : y;
-}
-
 // cos and sin of an angle of 2^20 or more by the library, out of line: its
 // registers are not the kernel's while the heads and weights wait in theirs
 __device__ __attribute__((noinline)) double2 sincos_far(float angle) {

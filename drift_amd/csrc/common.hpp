@@ -122,6 +122,28 @@ __device__ __forceinline__ double dpp_move(double v) {
 // mirrors (i <-> 7 - i, i <-> 15 - i) add the same partners as i ^ 4 and
 // i ^ 8. The order is fixed, so a row's sum does not depend on how many rows
 // share the launch.
+// 1 / sqrt(m) by the hardware's reciprocal square root and two Newton steps
+// (within a double ulp or two of the correctly rounded quotient of the
+// correctly rounded root, which moves an F32 result only where it lies that
+// close to a rounding boundary). Without a branch: a subnormal m is scaled
+// into range first (2^256 m, the result times 2^128), and 0 and infinity give
+// the division's own infinity and zero; NaN stays NaN. With NORMAL the caller
+// knows m is at least 2^-1000 or not a number (a positive epsilon is added to
+// it), and the scaling and the zero case are left out.
+template <bool NORMAL = false>
+__device__ __forceinline__ double inverse_sqrt(double m) {
+  const bool tiny = !NORMAL && m < 0x1p-1000;
+  const double ms = tiny ? m * 0x1p256 : m;
+  double y = __builtin_amdgcn_rsq(ms);
+  y = y * fma(-0.5 * ms * y, y, 1.5);
+  y = y * fma(-0.5 * ms * y, y, 1.5);
+  if constexpr (!NORMAL) {
+    y = tiny ? y * 0x1p128 : y;
+    y = m == 0.0 ? __builtin_huge_val() : y;
+  }
+  return m == __builtin_huge_val() ? 0.0 : y;
+}
+
 template <int width>
 __device__ __forceinline__ double group_sum(double v) {
   if constexpr (width > 1) v += dpp_move<0xb1>(v);   // quad_perm [1, 0, 3, 2]

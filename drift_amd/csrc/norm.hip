@@ -507,6 +507,7 @@ __global__ void __launch_bounds__(256) adaln_resident(const uint16_t* x, const f
       for (int j = 0; j < N; ++j) a[k][j] = 1.0 + (double)f[j];
     }
   }
+  const double inverse_cols = 1.0 / (double)cols;
   for (; row < end; row += waves_per_sample) {
     Raw next[K];
     if (row + waves_per_sample < end) load_row(row + waves_per_sample, next);
@@ -529,10 +530,14 @@ __global__ void __launch_bounds__(256) adaln_resident(const uint16_t* x, const f
     }
     s1 = group_sum<64>(s1);
     s2 = group_sum<64>(s2);
-    const double m1 = s1 / (double)cols;  // mean - x0
+    // the row's statistics are a chain the wave waits on, alone on its
+    // SIMD: the width's reciprocal (made once) for the two divisions, and
+    // 1/sqrt by the hardware's reciprocal root refined, not a root and a
+    // division (each within a double ulp or two)
+    const double m1 = s1 * inverse_cols;  // mean - x0
     const double mean = (double)x0 + m1;
-    const double variance = fmax(s2 / (double)cols - m1 * m1, 0.0);
-    const double factor = 1.0 / sqrt(variance + (double)eps);
+    const double variance = fmax(fma(s2, inverse_cols, -(m1 * m1)), 0.0);
+    const double factor = eps > 0.0f ? inverse_sqrt<true>(variance + (double)eps) : inverse_sqrt(variance + (double)eps);
     const double offset = -mean * factor;
 #pragma unroll
     for (int k = 0; k < K; ++k) {
