@@ -298,10 +298,12 @@ def make_kernels(hip: d.HipOps):
     table = torch.empty((rows, 6 * width), dtype=torch.float32, device=DEV)
     for lo in range(0, rows, 8192):
         table[lo:lo + 8192] = 0.3 * torch.randn((min(8192, rows - lo), 6 * width), generator=gen(9), device=DEV)
+    # in place, as every caller of the reference's modulateChunks runs it
+    # (models/Pid.scala:755,811, models/MageVae.scala:603)
     nbytes = rows * width * (2 + 2 + 4 + 4)
-    kernels.append(Kernel("modulate_chunks_bf16", "C5 per-row modulation out = x*(1+t[r][4])+t[r][3] bf16 [65520,3072], "
-                          "t F32 [65520,18432]", nbytes, rows,
-                          lambda i, n=n: hip.modulateChunks(xs5[i % n], table, 3, 4, outs5[i % n]), sets=n,
+    kernels.append(Kernel("modulate_chunks_bf16", "C5 per-row modulation x = x*(1+t[r][4])+t[r][3] in place, bf16 "
+                          "[65520,3072], t F32 [65520,18432]", nbytes, rows,
+                          lambda i, n=n: hip.modulateChunks(xs5[i % n], table, 3, 4, xs5[i % n]), sets=n,
                           read_bytes=rows * width * 10))
     nbytes = rows * width * (2 + 2 + 2 + 4)
     kernels.append(Kernel("gated_add_chunk_bf16", "C5 per-row gated residual x += t[r][5] * y bf16 [65520,3072]",
