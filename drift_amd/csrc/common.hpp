@@ -115,13 +115,15 @@ __device__ __forceinline__ double dpp_move(double v) {
   return __builtin_bit_cast(double, ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
 }
 
-// Sum over aligned groups of `width` lanes (a power of two up to 64); every
-// lane of a group gets the group's total. It is the xor butterfly (partners
-// i ^ 1, i ^ 2, ...), its steps inside 16-lane rows taken by DPP moves: after
-// the first two, the lanes of a quad hold one value, so the half-row and row
-// mirrors (i <-> 7 - i, i <-> 15 - i) add the same partners as i ^ 4 and
-// i ^ 8. The order is fixed, so a row's sum does not depend on how many rows
-// share the launch.
+// floor(i / d) for 0 <= i < 2^50 from a multiply by 1/d: the product is
+// within one of the quotient, and one step each way corrects it.
+__device__ __forceinline__ int64_t quotient(int64_t i, int64_t d, double inverse) {
+  int64_t q = (int64_t)((double)i * inverse);
+  q -= (q * d > i);
+  q += ((q + 1) * d <= i);
+  return q;
+}
+
 // 1 / sqrt(m) by the hardware's reciprocal square root and two Newton steps
 // (within a double ulp or two of the correctly rounded quotient of the
 // correctly rounded root, which moves an F32 result only where it lies that
@@ -144,6 +146,13 @@ __device__ __forceinline__ double inverse_sqrt(double m) {
   return m == __builtin_huge_val() ? 0.0 : y;
 }
 
+// Sum over aligned groups of `width` lanes (a power of two up to 64); every
+// lane of a group gets the group's total. It is the xor butterfly (partners
+// i ^ 1, i ^ 2, ...), its steps inside 16-lane rows taken by DPP moves: after
+// the first two, the lanes of a quad hold one value, so the half-row and row
+// mirrors (i <-> 7 - i, i <-> 15 - i) add the same partners as i ^ 4 and
+// i ^ 8. The order is fixed, so a row's sum does not depend on how many rows
+// share the launch.
 template <int width>
 __device__ __forceinline__ double group_sum(double v) {
   if constexpr (width > 1) v += dpp_move<0xb1>(v);   // quad_perm [1, 0, 3, 2]

@@ -292,7 +292,8 @@ __device__ __forceinline__ void store_chunk<Half>(Half* p, const float (&v)[8]) 
 // of zeros and sets *bad_id.
 template <typename T, typename F>
 __global__ void __launch_bounds__(256) decode_rows(const uint8_t* table, const int32_t* ids, T* out, int64_t count,
-                                                   int64_t vocab, int cols, int64_t row_bytes, int32_t* bad_id) {
+                                                   int64_t vocab, int cols, int64_t row_bytes, int32_t* bad_id,
+                                                   double row_inverse) {
   constexpr int kChunks = F::kValues / 8 > 0 ? F::kValues / 8 : 1;  // chunks per block
   __shared__ float lut[16];
   if constexpr (F::kLut != 0) {
@@ -303,7 +304,7 @@ __global__ void __launch_bounds__(256) decode_rows(const uint8_t* table, const i
   const int64_t total = count * per_row;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
-    const int64_t t = i / per_row;
+    const int64_t t = quotient(i, per_row, row_inverse);  // not a 64-bit division a chunk
     const int q = (int)(i - t * per_row);
     const int64_t id = ids ? ids[t] : t;
     float v[8];
@@ -328,11 +329,11 @@ __device__ __forceinline__ void store_value(Half* p, float v) { p->bits = __buil
 
 template <typename T, int FORMAT>
 __global__ void __launch_bounds__(256) dense_values(const uint8_t* table, const int32_t* ids, T* out, int64_t count,
-                                                    int64_t vocab, int cols, int32_t* bad_id) {
+                                                    int64_t vocab, int cols, int32_t* bad_id, double col_inverse) {
   const int64_t total = count * cols;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
-    const int64_t t = i / cols;
+    const int64_t t = quotient(i, cols, col_inverse);
     const int64_t id = ids ? ids[t] : t;
     float v = 0.0f;
     if (id < 0 || id >= vocab) {
@@ -516,13 +517,13 @@ int decode_launch(const char* entry, const void* table, int32_t format, const in
     const auto* bytes = static_cast<const uint8_t*>(table);
     if (format == DRIFT_F32)
       hipLaunchKernelGGL((dense_values<T, DRIFT_F32>), grid, dim3(256), 0, s, bytes, ids, out, count, vocab, cols,
-                         bad_id);
+                         bad_id, 1.0 / (double)cols);
     else if (format == DRIFT_F16)
       hipLaunchKernelGGL((dense_values<T, DRIFT_F16>), grid, dim3(256), 0, s, bytes, ids, out, count, vocab, cols,
-                         bad_id);
+                         bad_id, 1.0 / (double)cols);
     else
       hipLaunchKernelGGL((dense_values<T, DRIFT_BF16>), grid, dim3(256), 0, s, bytes, ids, out, count, vocab, cols,
-                         bad_id);
+                         bad_id, 1.0 / (double)cols);
     return launched(entry);
   }
   if (!aligned16(out)) return refuse("%s: out is not 16-byte aligned", entry);
@@ -550,7 +551,7 @@ int decode_launch(const char* entry, const void* table, int32_t format, const in
       }                                                                                                          \
     }                                                                                                            \
     hipLaunchKernelGGL((decode_rows<T, F>), grid, dim3(256), 0, s, bytes, ids, out, count, vocab, cols, row_bytes, \
-                       bad_id);                                                                                  \
+                       bad_id, 1.0 / (double)(cols / 8));                                                        \
     break;
     DRIFT_DECODE(DRIFT_F32, Dense<DRIFT_F32>)
     DRIFT_DECODE(DRIFT_F16, Dense<DRIFT_F16>)

@@ -39,15 +39,6 @@ struct RowMap {
   double per_inverse;  // 1 / per
 };
 
-// floor(i / d) for 0 <= i < 2^50 from a multiply by 1/d: the product is
-// within one of the quotient, and one step each way corrects it.
-__device__ __forceinline__ int64_t quotient(int64_t i, int64_t d, double inverse) {
-  int64_t q = (int64_t)((double)i * inverse);
-  q -= (q * d > i);
-  q += ((q + 1) * d <= i);
-  return q;
-}
-
 // N consecutive F32 factors. A row's table chunk is read once (streamed); a
 // sample's gate row is read by every row of the sample (cached).
 template <int N, bool STREAM>
