@@ -41,7 +41,9 @@ each kernel is also replayed in alternation with its best probe
 ratio under the same conditions);
 `roofline` is the dominant kernel's; `cpu_baseline` is the CPU reference
 arithmetic (the oracle) timed on a bounded sample of the same work on this
-host's cores, scaled to the whole step.
+host's cores, scaled to the whole step. With `--formats`, `formats` holds
+every storage type's decode of a [14336, 4096] weight to bf16, each against
+its probe in alternation (not part of the step or `value`).
 """
 
 from __future__ import annotations
@@ -361,6 +363,60 @@ def make_kernels(hip: d.HipOps):
 
 
 # ------------------------------------------------------------------ CPU baseline
+
+def format_kernels(hip: d.HipOps) -> list:
+    """Every storage type's whole-table decode to bf16 (the GEMM path's
+    dequantize) at the Q4_K weight's shape [14336, 4096]: random bytes with
+    each block's leading fp16 fields set to small positive scales, buffer
+    sets past the MALL. Timed only with --formats, outside the step."""
+    rows, cols = 14336, 4096
+    kernels = []
+    for name, t in d.STORAGE_TYPES.items():
+        row_bytes = t.rowBytes(cols)
+        nbytes = rows * row_bytes + rows * cols * 2
+        n = sets_for(nbytes)
+        tables = []
+        for i in range(n):
+            g = gen(2000 + i)
+            raw = torch.randint(0, 256, (rows, row_bytes), generator=g, device=DEV, dtype=torch.int32).to(torch.uint8)
+            if t.values > 1 and name != "Q6_K":  # Q6_K keeps its scale last
+                blocks = raw.view(rows, cols // t.values, t.bytes)
+                scales = (1e-3 + 1e-2 * torch.rand((rows, cols // t.values, 2), generator=g, device=DEV)).half()
+                blocks[:, :, 0:4] = scales.view(torch.uint8).view(rows, cols // t.values, 4)
+            tables.append(d.StoredTable(raw, t, cols))
+        outs = [torch.empty((rows, cols), dtype=torch.bfloat16, device=DEV) for _ in range(n)]
+        kernels.append(Kernel(f"dequantize_{name.lower()}_bf16", f"{name} weight [14336,4096] decoded to bf16", nbytes,
+                              rows, lambda i, n=n, ts=tables, os_=outs: hip.dequantize(ts[i % n], os_[i % n]), sets=n,
+                              read_bytes=rows * row_bytes))
+    return kernels
+
+
+def time_formats(hip: d.HipOps, lib, steps: int, warmup: int) -> dict:
+    """--formats: each storage type's decode timed from a graph and against
+    its best stream probe in alternation."""
+    kernels = format_kernels(hip)
+    for k in kernels:
+        k.prepare(hip)
+    probes = {k.name: ceiling_probes(k, lib) for k in kernels}
+    time_graphs(kernels, steps, warmup)
+    time_graphs([p for group in probes.values() for p in group], steps, warmup)
+    for k in kernels:
+        k.ceiling = min(probes[k.name], key=lambda p: p.graph_ms)
+    time_matched([[k, k.ceiling] for k in kernels], steps, MATCHED_ROUNDS)
+    out = {}
+    for k in kernels:
+        gbs = k.bytes / (k.graph_ms * 1e-3) / 1e9
+        out[k.name] = {"config": k.config, "us": round(k.graph_ms * 1e3, 2), "bytes": k.bytes, "GB_s": round(gbs, 1),
+                       "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "probe_us": round(k.ceiling.matched_ms * 1e3, 2),
+                       "frac_of_probe_matched": round(k.ceiling.matched_ms / k.matched_ms, 4)}
+    for k in kernels:
+        k.calls = []
+    for group in probes.values():
+        for p in group:
+            p.buffers = None
+    torch.cuda.synchronize()
+    return out
+
 
 def host_cpu() -> str:
     try:
@@ -712,6 +768,8 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=24.0, help="seconds of CPU reference work, about")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="", help="comma-separated kernel names to run (profiling)")
+    ap.add_argument("--formats", action="store_true",
+                    help="also time every storage type's decode to bf16 (outside the step), reported in 'formats'")
     ap.add_argument("--no-host", action="store_true",
                     help="skip the host cost per call (a child process that launches kernels of its own: profilers "
                          "tracing this process would trace it too)")
@@ -818,6 +876,7 @@ def main():
     del src, dsts
 
     host = None if args.only or args.no_host else host_call_cost()
+    formats = time_formats(hip, lib, args.steps, args.warmup) if args.formats else None
 
     if not args.no_cpu:
         cpu_baseline(kernels, args.cpu_budget)
@@ -870,6 +929,7 @@ def main():
         },
         "kernels": table,
         "ceilings": ceilings,
+        "formats": formats,
         "hbm_copy_reference": {"GB_s": round(copy_gbs, 1), "frac_hbm_peak": round(copy_gbs / HBM_PEAK_GBS, 4),
                                "what": "torch copy_ of 402.6 MB (read + write)"},
         "host_us_per_call": host,
