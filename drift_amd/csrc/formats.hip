@@ -404,41 +404,75 @@ __global__ void __launch_bounds__(256) decode_staged(const uint8_t* table, const
   }
 }
 
-// The 256-value formats a run of 8 blocks at a time, for rows of whole runs
-// on 16-byte boundaries: a one-wave block copies the run's bytes (8 x 136 to
-// 8 x 210, a multiple of 16) into LDS with two 16-byte loads a lane, all in
-// flight together, then each lane decodes 4 chunks (chunk k * 64 + lane of
-// the run's 256) from there, so each store instruction writes 64
-// consecutive 16-byte pieces. decode_staged's 4-byte copies of one block
-// per half wave keep too few bytes in flight to cover HBM's latency.
-constexpr int kRunBlocks = 8;
+// Block formats a run of 2048 values at a time (8 blocks of 256 or 64 of 32),
+// for rows of whole runs on 16-byte boundaries: a one-wave block copies the
+// run's bytes (1,088 to 1,680 for the formats that take it, a multiple of 16)
+// into LDS with 16-byte loads, all in flight together, then each lane decodes
+// 4 chunks (chunk k * 64 + lane of the run's 256) from there, so each store
+// instruction writes 64 consecutive 16-byte pieces. decode_staged's 4-byte
+// copies of one block per half wave keep too few bytes in flight to cover
+// HBM's latency.
+constexpr int kRunValues = 2048;
 
 template <typename F>
 constexpr int run_pieces() {
-  return kRunBlocks * F::kBytes / 16;
+  return kRunValues / F::kValues * F::kBytes / 16;
 }
+
+// a run's blocks start every kBytes from a 16-byte boundary: the largest
+// power of two dividing kBytes, at most 8, is each one's alignment
+template <typename F>
+constexpr int run_field_align() {
+  return (F::kBytes & -F::kBytes) < 8 ? (F::kBytes & -F::kBytes) : 8;
+}
+
+// Whether a format's rows of whole runs take decode_runs rather than
+// decode_rows. Each 32-value format was timed both ways on a [14336, 4096]
+// weight decoded to bf16, launches of the two interleaved (median us,
+// decode_rows / decode_runs): Q5_1 29.5 / 26.6, IQ4_NL 27.2 / 25.7, ROCmFP4
+// 28.9 / 25.8 and ROCmFP4 fast 28.6 / 26.9 take runs; Q4_1 24.1 / 25.7 and
+// Q8_0 25.3 / 29.6 keep decode_rows, as do Q4_0 (25.4 / 25.3) and Q5_0
+// (30.9 / 30.6), even. The 256-value formats all take runs.
+template <typename F>
+struct TakesRuns {
+  static constexpr bool value = F::kValues == 256;
+};
+template <>
+struct TakesRuns<Q5<true>> {
+  static constexpr bool value = true;
+};
+template <>
+struct TakesRuns<IQ4_NL> {
+  static constexpr bool value = true;
+};
+template <bool FAST>
+struct TakesRuns<RocmFp4<FAST>> {
+  static constexpr bool value = true;
+};
 
 template <typename T, typename F>
 __global__ void __launch_bounds__(kWave) decode_runs(const uint8_t* table, const int32_t* ids, T* out, int64_t count,
                                                      int64_t vocab, int cols, int64_t row_bytes, int32_t* bad_id) {
-  static_assert(F::kValues == 256 && (kRunBlocks * F::kBytes) % 16 == 0, "runs of whole 16-byte pieces");
+  static_assert(F::kValues >= 8 && (kRunValues / F::kValues * F::kBytes) % 16 == 0, "runs of whole 16-byte pieces");
   constexpr int kPieces = run_pieces<F>();
   constexpr int kLoads = (kPieces + kWave - 1) / kWave;
-  constexpr int kFieldAlign = F::kBytes % 8 == 0 ? 8 : 2;  // where the run puts each block
+  constexpr int kFieldAlign = run_field_align<F>();
+  constexpr int kBlockChunks = F::kValues / 8;
+  static_assert(kFieldAlign >= F::kAlign, "the run keeps each block's alignment");
   __shared__ __align__(16) uint8_t staged[kPieces * 16];
   __shared__ float lut[16];
   const int lane = (int)threadIdx.x;
   if constexpr (F::kLut != 0) {
     if (lane < 16) lut[lane] = lut_entry(F::kLut, lane);
   }
-  const int runs_per_row = cols / (256 * kRunBlocks);
+  const int runs_per_row = cols / kRunValues;
   const int64_t run = blockIdx.x;
   const int64_t t = run / runs_per_row;
   const int r = (int)(run - t * runs_per_row);
   const int64_t id = ids ? ids[t] : t;
   const bool bad = id < 0 || id >= vocab;
-  const uint4* src =
-      reinterpret_cast<const uint4*>(table + (bad ? 0 : id) * row_bytes + (int64_t)r * kRunBlocks * F::kBytes);
+  const uint4* src = reinterpret_cast<const uint4*>(table + (bad ? 0 : id) * row_bytes +
+                                                    (int64_t)r * (kRunValues / F::kValues) * F::kBytes);
   uint4 piece[kLoads];
 #pragma unroll
   for (int k = 0; k < kLoads; ++k) piece[k] = stream_load(src + min(lane + k * kWave, kPieces - 1));
@@ -447,7 +481,7 @@ __global__ void __launch_bounds__(kWave) decode_runs(const uint8_t* table, const
     if (lane + k * kWave < kPieces) reinterpret_cast<uint4*>(staged)[lane + k * kWave] = piece[k];
   wave_sync();
   if (bad && bad_id && lane == 0) *bad_id = 1;
-  T* target = out + t * cols + (int64_t)r * kRunBlocks * 256;
+  T* target = out + t * cols + (int64_t)r * kRunValues;
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     const int chunk = k * kWave + lane;
@@ -456,7 +490,7 @@ __global__ void __launch_bounds__(kWave) decode_runs(const uint8_t* table, const
 #pragma unroll
       for (int i = 0; i < 8; ++i) v[i] = 0.0f;
     } else {
-      F::template decode<kFieldAlign>(staged + (chunk >> 5) * F::kBytes, chunk & 31, v, lut);
+      F::template decode<kFieldAlign>(staged + (chunk / kBlockChunks) * F::kBytes, chunk % kBlockChunks, v, lut);
     }
     store_chunk<T>(target + chunk * 8, v);
   }
@@ -536,13 +570,15 @@ int decode_launch(const char* entry, const void* table, int32_t format, const in
   switch (format) {
 #define DRIFT_DECODE(CODE, F)                                                                                     \
   case CODE:                                                                                                     \
-    if constexpr (F::kValues == 256) {                                                                           \
-      const int64_t runs = count * (cols / (256 * kRunBlocks));                                                  \
-      if (vocab > 0 && cols % (256 * kRunBlocks) == 0 && aligned16(table) && runs <= kOneShotBlocks) {           \
+    if constexpr (TakesRuns<F>::value) {                                                                        \
+      const int64_t runs = count * (cols / kRunValues);                                                          \
+      if (vocab > 0 && cols % kRunValues == 0 && aligned16(table) && runs <= kOneShotBlocks) {                   \
         hipLaunchKernelGGL((decode_runs<T, F>), dim3((unsigned)runs), dim3(kWave), 0, s, bytes, ids, out, count,  \
                            vocab, cols, row_bytes, bad_id);                                                      \
         break;                                                                                                   \
       }                                                                                                          \
+    }                                                                                                            \
+    if constexpr (F::kValues == 256) {                                                                           \
       if (vocab > 0) {                                                                                           \
         const dim3 staged(grid_for(count * (cols / 256), 8, kOneShotBlocks));                                    \
         hipLaunchKernelGGL((decode_staged<T, F>), staged, dim3(256), 0, s, bytes, ids, out, count, vocab, cols,    \

@@ -69,15 +69,18 @@ def test_dequantize_every_storage_type(hip, name, out_type):
     assert_bits(expected, host_bits(out), what=f"{name} dequantize {out_type}")
 
 
-RUN_FORMATS = [n for n in NAMES if d.STORAGE_TYPES[n].values == 256]
+# every block format: those that decode rows of whole runs staged in LDS, and
+# those that keep the chunk-a-thread decoder there (Q4_0, Q4_1, Q5_0, Q8_0)
+RUN_FORMATS = [n for n in NAMES if d.STORAGE_TYPES[n].values > 1]
 
 
 @pytest.mark.parametrize("name", RUN_FORMATS)
 @pytest.mark.parametrize("cols", [2048, 6144])
 def test_rows_of_whole_runs(hip, name, cols):
-    # rows of whole runs of 8 blocks, the table on a 16-byte boundary: the
-    # run decoder, for the gather (with ids outside the table: zero rows and
-    # the flag) and the whole-table decode
+    # rows of whole runs of 2048 values (8 blocks of 256 or 64 of 32), the
+    # table on a 16-byte boundary: the run decoder where the format takes it,
+    # for the gather (with ids outside the table: zero rows and the flag) and
+    # the whole-table decode
     vocab = 19
     raw, table = table_of(name, vocab, cols, 41 + cols)
     assert table.data.data_ptr() % 16 == 0
@@ -108,7 +111,8 @@ def test_rows_of_whole_runs(hip, name, cols):
 @pytest.mark.parametrize("name", RUN_FORMATS)
 def test_runs_off_a_16_byte_boundary(hip, name):
     # the same rows from a table 8 bytes past a 16-byte boundary: the
-    # one-block-a-half-wave decoder, with the same result
+    # one-block-a-half-wave decoder (256-value blocks) or the chunk-a-thread
+    # one (32-value blocks), with the same result
     vocab, cols = 7, 2048
     raw, _ = table_of(name, vocab, cols, 77)
     t = d.STORAGE_TYPES[name]
