@@ -205,6 +205,19 @@ def test_attention_inputs_small_heads(hip, dtype, heads, kv, dim, gated):
     run_attention_inputs(hip, dtype, t, heads, kv, dim, rope, start, table, pages, gated, 120 + dim)
 
 
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("heads,kv,dim", [(16, 3, 128), (64, 16, 64), (32, 9, 128)])
+def test_attention_inputs_key_heads_by_the_group(hip, dtype, heads, kv, dim):
+    # no gate, whole waves of query heads; key heads that fill part of a
+    # wave's group, two groups, a group and a part
+    t, start = 29, 7
+    step(f"attentionInputs {dtype} heads {heads}/{kv} of {dim}, {t} tokens")
+    pages = -(-(start + t) // PAGE) + 1
+    table = np.random.default_rng(heads + kv).permutation(pages).astype(np.int32)
+    rope = d.Rope(1e6, dim, d.RopeLayout.Neox, d.RopeSections.Single())
+    run_attention_inputs(hip, dtype, t, heads, kv, dim, rope, start, table, pages, False, 170 + kv)
+
+
 def test_attention_inputs_flag_a_page_outside_the_cache(hip):
     step("attentionInputs with a page-table entry past the cache")
     t, heads, kv, dim = 4, 4, 2, 128
