@@ -77,12 +77,15 @@ def test_embedding(hip, name, four_bit, group_size, one_scale, out_type):
         same_bits(o.to_bf16(want), host_bits(out), f"{name} bf16")
 
 
-@pytest.mark.parametrize("name,four_bit,group_size,one_scale", CASES)
-@pytest.mark.parametrize("shape", [(1, 256), (23, 768), (64, 3072)])
+# every case at every shape whose rows its groups divide
+DEQUANTIZE_CASES = [case + (shape,) for case in CASES for shape in [(1, 256), (23, 768), (64, 3072)]
+                    if not case[1] or shape[1] % case[2] == 0]
+
+
+@pytest.mark.parametrize("name,four_bit,group_size,one_scale,shape", DEQUANTIZE_CASES,
+                         ids=[f"{c[0]} [{c[4][0]},{c[4][1]}]" for c in DEQUANTIZE_CASES])
 def test_dequantize(hip, name, four_bit, group_size, one_scale, shape):
     rows, cols = shape
-    if four_bit and cols % group_size:
-        pytest.skip("groups do not divide the row")
     r = o.random_rotated(rows, cols, np.random.default_rng(41 + cols), four_bit, group_size or 32, one_scale)
     table = device_table(hip, r)
     step(f"rotated dequantize {name} [{rows}, {cols}]")
