@@ -33,8 +33,10 @@ and writes of the tensors each op names) over the step's wall time;
 peak, fraction of its ceiling and rows/s; `ceilings` is the streaming probe
 (drift_stream_mix) moving each long kernel's bytes in its read:write mix,
 for the gather also its own pattern with no decode (drift_row_probe: the
-rows its ids name read, its output written; `frac_of_row_probe`), and the
-reference's streaming read (drift_read_sum_f32x4) over 1 GiB. A probe's
+rows its ids name read, its output written; `frac_of_row_probe`), the
+reference's streaming read (drift_read_sum_f32x4) over 1 GiB, and the
+per-launch floor of a graph replay (`launch_floor`: one block writing one
+16-byte chunk), which the decode shapes' few microseconds sit on. A probe's
 launches fall into two or three durations by clock and memory state, so
 each kernel is also replayed in alternation with its best probe
 (`ceilings[k]["matched"]`, and `frac_of_probe_matched`: the median replays'
@@ -642,6 +644,20 @@ def row_probe(k: Kernel, lib) -> Kernel:
     return probe
 
 
+def floor_probe(lib) -> Kernel:
+    """The per-launch floor of a graph replay: drift_stream_mix writing one
+    16-byte chunk (one block of 256 threads) and reading nothing. The decode
+    shapes (C2) move tens of kilobytes: their time is this floor plus their
+    own dependent chain (loads, a row reduction, the stores)."""
+    dsts = [torch.empty(16, dtype=torch.uint8, device=DEV) for _ in range(2)]
+    probe = Kernel("launch_floor", "drift_stream_mix writing one 16-byte chunk, nothing read: one block of 256 "
+                   "threads", 16, 1, None, 2, read_bytes=0)
+    probe.buffers = dsts
+    for dst in dsts:
+        probe.calls.append(("drift_stream_mix", lib.drift_stream_mix, (None, 0, ctypes.c_void_p(dst.data_ptr()), 1, 1)))
+    return probe
+
+
 def read_probe(lib, gib_bytes: int, blocks: int, name: str) -> Kernel:
     """The reference's streaming read (drift_read_sum_f32x4) over gib_bytes."""
     x = torch.ones(gib_bytes // 4, dtype=torch.float32, device=DEV)
@@ -802,6 +818,7 @@ def main():
                 rows_probes[k.name] = p
     reads = [] if args.only else [read_probe(lib, 1 << 30, 2048, "read_sum_1gib_2048_blocks"),
                                   read_probe(lib, 1 << 30, (1 << 30) // 16 // 1024, "read_sum_1gib_one_pass")]
+    floors = [] if args.only else [floor_probe(lib)]
     torch.cuda.synchronize()
 
     # kernels: graph replays (kernel time) and Python-driven launches (what a
@@ -812,8 +829,8 @@ def main():
     largest_first = sorted(kernels, key=lambda k: k.bytes, reverse=True)
     wall = time_graphs(largest_first, args.steps, args.warmup)
     time_eager(largest_first, args.steps)
-    time_graphs([p for group in probes.values() for p in group] + list(rows_probes.values()) + reads, args.steps,
-                args.warmup)
+    time_graphs([p for group in probes.values() for p in group] + list(rows_probes.values()) + reads + floors,
+                args.steps, args.warmup)
     ceilings = {}
     for k in kernels:
         if k.name not in probes:
@@ -847,12 +864,14 @@ def main():
         gbs = r.bytes / (r.graph_ms * 1e-3) / 1e9
         ceilings[r.name] = {"bytes": r.bytes, "us": round(r.graph_ms * 1e3, 2), "GB_s": round(gbs, 1),
                             "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "what": r.config}
+    for f in floors:
+        ceilings[f.name] = {"us": round(f.graph_ms * 1e3, 2), "what": f.config}
     for group in probes.values():
         for p in group:
             p.buffers = None
-    for r in reads:
+    for r in reads + floors:
         r.buffers = None
-    probes = reads = rows_probes = None
+    probes = reads = rows_probes = floors = None
     torch.cuda.synchronize()
 
     # A plain device copy of one C5 tensor (402.6 MB read + 402.6 MB
