@@ -289,8 +289,10 @@ __device__ __forceinline__ void store_chunk<Half>(Half* p, const float (&v)[8]) 
 
 // Rows ids[t] (row t with no ids) of a table of format F into out [count,
 // cols], a thread per chunk of 8 values. An id outside [0, vocab) gets a row
-// of zeros and sets *bad_id.
-template <typename T, typename F>
+// of zeros and sets *bad_id. BY_ROW: the grid's y is the row (at most 65535
+// rows) and its x the row's blocks of 256 chunks, so no thread divides; else
+// a one-dimensional grid over every chunk, the row by a reciprocal quotient.
+template <typename T, typename F, bool BY_ROW = false>
 __global__ void __launch_bounds__(256) decode_rows(const uint8_t* table, const int32_t* ids, T* out, int64_t count,
                                                    int64_t vocab, int cols, int64_t row_bytes, int32_t* bad_id,
                                                    double row_inverse) {
@@ -301,11 +303,7 @@ __global__ void __launch_bounds__(256) decode_rows(const uint8_t* table, const i
     __syncthreads();
   }
   const int per_row = cols / 8;
-  const int64_t total = count * per_row;
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
-    const int64_t t = quotient(i, per_row, row_inverse);  // not a 64-bit division a chunk
-    const int q = (int)(i - t * per_row);
+  auto chunk = [&](int64_t t, int q) {
     const int64_t id = ids ? ids[t] : t;
     float v[8];
     if (id < 0 || id >= vocab) {
@@ -318,6 +316,17 @@ __global__ void __launch_bounds__(256) decode_rows(const uint8_t* table, const i
       F::decode(table + id * row_bytes + (int64_t)(q / kChunks) * F::kBytes, q % kChunks, v, lut);
     }
     store_chunk<T>(out + t * cols + (int64_t)q * 8, v);
+  };
+  if constexpr (BY_ROW) {
+    const int q = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+    if (q < per_row) chunk((int64_t)blockIdx.y, q);
+  } else {
+    const int64_t total = count * per_row;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+      const int64_t t = quotient(i, per_row, row_inverse);  // not a 64-bit division a chunk
+      chunk(t, (int)(i - t * per_row));
+    }
   }
 }
 
@@ -351,11 +360,14 @@ __global__ void __launch_bounds__(256) dense_values(const uint8_t* table, const 
   }
 }
 
-// The 256-value formats (the K-quants, IQ4_XS) through LDS: each half wave
-// copies one block (144 to 210 bytes) into LDS with a few coalesced 4- or
-// 2-byte loads a lane, then its 32 lanes decode their chunks from there, so
-// the block's scales and fields are read from HBM once, not by every lane
-// with its own small loads. Two blocks a wave, waves independent.
+// The 256-value formats (the K-quants, IQ4_XS) through LDS, for more rows
+// than decode_rows' two-dimensional grid holds: each half wave copies one
+// block (144 to 210 bytes) into LDS with a few coalesced 4- or 2-byte loads a
+// lane, then its 32 lanes decode their chunks from there, so the block's
+// scales and fields are read from HBM once, not by every lane with its own
+// small loads. Two blocks a wave, waves independent. (At [14336, 4096] the
+// two-dimensional decode_rows beat it for every 256-value format: Q4_K 25.3
+// against 27.3 us, Q6_K 26.8 against 32.3, IQ4_XS 23.2 against 29.1.)
 template <typename T, typename F>
 __global__ void __launch_bounds__(256) decode_staged(const uint8_t* table, const int32_t* ids, T* out, int64_t count,
                                                      int64_t vocab, int cols, int64_t row_bytes, int32_t* bad_id) {
@@ -406,13 +418,15 @@ __global__ void __launch_bounds__(256) decode_staged(const uint8_t* table, const
 
 // Block formats a run of 2048 values at a time (8 blocks of 256 or 64 of 32),
 // for rows of whole runs on 16-byte boundaries: a one-wave block copies the
-// run's bytes (1,088 to 1,680 for the formats that take it, a multiple of 16)
+// run's bytes (1,152 to 1,408 for the formats that take it, a multiple of 16)
 // into LDS with 16-byte loads, all in flight together, then each lane decodes
 // 4 chunks (chunk k * 64 + lane of the run's 256) from there, so each store
-// instruction writes 64 consecutive 16-byte pieces. decode_staged's 4-byte
-// copies of one block per half wave keep too few bytes in flight to cover
-// HBM's latency.
+// instruction writes 64 consecutive 16-byte pieces and a block's scales are
+// read from LDS by the lanes that share them.
 constexpr int kRunValues = 2048;
+
+// rows a grid's y dimension holds (decode_rows' BY_ROW form)
+constexpr int64_t kMaxGridRows = 65535;
 
 template <typename F>
 constexpr int run_pieces() {
@@ -427,26 +441,26 @@ constexpr int run_field_align() {
 }
 
 // Whether a format's rows of whole runs take decode_runs rather than
-// decode_rows. Each 32-value format was timed both ways on a [14336, 4096]
-// weight decoded to bf16, launches of the two interleaved (median us,
-// decode_rows / decode_runs): Q5_1 29.5 / 26.6, IQ4_NL 27.2 / 25.7, ROCmFP4
-// 28.9 / 25.8 and ROCmFP4 fast 28.6 / 26.9 take runs; Q4_1 24.1 / 25.7 and
-// Q8_0 25.3 / 29.6 keep decode_rows, as do Q4_0 (25.4 / 25.3) and Q5_0
-// (30.9 / 30.6), even. The 256-value formats all take runs.
+// decode_rows by row (its two-dimensional grid). Timed on a [14336, 4096]
+// weight decoded to bf16, the two decoders' graph replays alternating with
+// the format's stream probe, both orders (us, runs / by row): Q4_K 25.0 /
+// 28.1, Q5_K 26.4 / 32.9, IQ4_NL 25.3 / 25.7 and ROCmFP4 25.4 / 26.9 take
+// runs; Q5_1 26.6 / 25.7, Q6_K 30.8 / 29.7, IQ4_XS 27.3 / 26.3 and ROCmFP4
+// fast 27.4 / 27.0 decode by row, as do Q4_0, Q4_1, Q5_0 and Q8_0.
 template <typename F>
 struct TakesRuns {
-  static constexpr bool value = F::kValues == 256;
+  static constexpr bool value = false;
 };
-template <>
-struct TakesRuns<Q5<true>> {
+template <bool FIVE>
+struct TakesRuns<QK45<FIVE>> {
   static constexpr bool value = true;
 };
 template <>
 struct TakesRuns<IQ4_NL> {
   static constexpr bool value = true;
 };
-template <bool FAST>
-struct TakesRuns<RocmFp4<FAST>> {
+template <>
+struct TakesRuns<RocmFp4<false>> {
   static constexpr bool value = true;
 };
 
@@ -578,6 +592,11 @@ int decode_launch(const char* entry, const void* table, int32_t format, const in
         break;                                                                                                   \
       }                                                                                                          \
     }                                                                                                            \
+    if (count <= kMaxGridRows) {                                                                                 \
+      hipLaunchKernelGGL((decode_rows<T, F, true>), dim3((unsigned)ceil_div(cols / 8, 256), (unsigned)count),      \
+                         dim3(256), 0, s, bytes, ids, out, count, vocab, cols, row_bytes, bad_id, 0.0);           \
+      break;                                                                                                       \
+    }                                                                                                              \
     if constexpr (F::kValues == 256) {                                                                           \
       if (vocab > 0) {                                                                                           \
         const dim3 staged(grid_for(count * (cols / 256), 8, kOneShotBlocks));                                    \

@@ -69,8 +69,9 @@ def test_dequantize_every_storage_type(hip, name, out_type):
     assert_bits(expected, host_bits(out), what=f"{name} dequantize {out_type}")
 
 
-# every block format: those that decode rows of whole runs staged in LDS, and
-# those that keep the chunk-a-thread decoder there (Q4_0, Q4_1, Q5_0, Q8_0)
+# every block format: those that decode rows of whole runs staged in LDS
+# (Q4_K, Q5_K, IQ4_NL, ROCmFP4), and those that decode them a chunk a thread
+# by row
 RUN_FORMATS = [n for n in NAMES if d.STORAGE_TYPES[n].values > 1]
 
 
@@ -111,8 +112,7 @@ def test_rows_of_whole_runs(hip, name, cols):
 @pytest.mark.parametrize("name", RUN_FORMATS)
 def test_runs_off_a_16_byte_boundary(hip, name):
     # the same rows from a table 8 bytes past a 16-byte boundary: the
-    # one-block-a-half-wave decoder (256-value blocks) or the chunk-a-thread
-    # one (32-value blocks), with the same result
+    # chunk-a-thread decoder by row, with the same result
     vocab, cols = 7, 2048
     raw, _ = table_of(name, vocab, cols, 77)
     t = d.STORAGE_TYPES[name]
@@ -126,6 +126,24 @@ def test_runs_off_a_16_byte_boundary(hip, name):
     hip.embedding(table, dev_i32(ids), out)
     want = o.embedding(name, raw, vocab, cols, ids)
     assert_bits(want.view(np.uint32), host_f32(out).view(np.uint32), what=f"{name} f32 off 16")
+
+
+@pytest.mark.parametrize("name", NAMES)
+def test_more_rows_than_a_grid_column(hip, name):
+    # 65,543 ids, more rows than the by-row grid's 65,535: the
+    # one-dimensional decoders (the one-block-a-half-wave decoder for the
+    # 256-value formats), every value of the output against the oracle
+    values = d.STORAGE_TYPES[name].values
+    cols = 256 if values > 1 else 40
+    vocab = 23
+    raw, table = table_of(name, vocab, cols, 91)
+    ids = np.random.default_rng(92).integers(0, vocab, 65543).astype(np.int32)
+    ids[[0, -1]] = [vocab - 1, 0]
+    step(f"embedding {name} -> bf16, {ids.size} ids of {cols} values")
+    out = torch.empty((ids.size, cols), dtype=torch.bfloat16, device=DEV)
+    hip.embedding(table, dev_i32(ids), out)
+    rows = o.to_bf16(o.embedding(name, raw, vocab, cols, np.arange(vocab, dtype=np.int32)))
+    assert_bits(rows[ids], host_bits(out), what=f"{name} {ids.size} rows")
 
 
 @pytest.mark.parametrize("name", ["Q4_K", "IQ4_NL", "Q4_0_ROCMFP4_FAST"])
