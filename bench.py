@@ -605,43 +605,62 @@ def cpu_baseline(kernels, budget_s: float):
 # ------------------------------------------------------------------ ceilings
 
 def ceiling_probes(k: Kernel, lib) -> list:
-    """The stream probe (drift_stream_mix) moving k's read and write bytes
-    with 1, 2 and 4 chunks a lane, over buffer sets totalling more than
-    512 MB like the kernel's; the fastest is k's ceiling."""
+    """The probes moving k's read and write bytes with nothing else, over
+    buffer sets totalling more than 512 MB like the kernel's: the stream
+    probe (drift_stream_mix: 256-thread blocks that only read or only write,
+    1, 2 or 4 chunks a lane) and the one-wave probe (drift_wave_copy: each
+    one-wave block reading its share and then writing its share, 1, 2, 4 or
+    8 chunks a lane, the shape the fused kernels take). The fastest is k's
+    ceiling."""
     reads = -(-k.read_bytes // 16)
     writes = -(-(k.bytes - k.read_bytes) // 16)
     n = sets_for(16 * (reads + writes))
     buffers = [(torch.empty(max(reads, 1) * 16, dtype=torch.uint8, device=DEV).fill_(7),
                 torch.empty(writes * 16, dtype=torch.uint8, device=DEV)) for _ in range(n)]
     probes = []
-    for per in (1, 2, 4):
-        probe = Kernel(f"ceiling of {k.name}", f"{reads} chunks read, {writes} written, {per} a lane",
-                       16 * (reads + writes), k.rows, None, n, read_bytes=16 * reads)
-        probe.per_lane = per
-        probe.buffers = buffers
-        for src, dst in buffers:
-            probe.calls.append(("drift_stream_mix", lib.drift_stream_mix,
-                                (ctypes.c_void_p(src.data_ptr()), reads, ctypes.c_void_p(dst.data_ptr()), writes, per)))
-        probes.append(probe)
+    for entry, shape, lanes in (("drift_stream_mix", "stream_mix", (1, 2, 4)),
+                                ("drift_wave_copy", "wave_copy", (1, 2, 4, 8))):
+        for per in lanes:
+            probe = Kernel(f"ceiling of {k.name}", f"{shape}: {reads} chunks read, {writes} written, {per} a lane",
+                           16 * (reads + writes), k.rows, None, n, read_bytes=16 * reads)
+            probe.per_lane = per
+            probe.shape = shape
+            probe.buffers = buffers
+            for src, dst in buffers:
+                probe.calls.append((entry, getattr(lib, entry),
+                                    (ctypes.c_void_p(src.data_ptr()), reads, ctypes.c_void_p(dst.data_ptr()), writes,
+                                     per)))
+            probes.append(probe)
     return probes
 
 
-def row_probe(k: Kernel, lib) -> Kernel:
-    """The gather's own pattern with no decode (drift_row_probe): each of
-    k's launches (table, ids, out, count, vocab, cols, bad_id) becomes a
-    block per id reading the whole Q8_0 row the id names and writing the
-    row's BF16 bytes, with the same ids and outputs. Random rows of a table
-    larger than the cache come from scattered DRAM pages, which the stream
-    probe's contiguous reads do not measure."""
-    probe = Kernel(f"row probe of {k.name}", "rows of the gather's table read at its ids, its output written",
-                   k.bytes, k.rows, None, k.sets, read_bytes=k.read_bytes)
-    for _, _, (table, ids, out, count, vocab, cols, _) in k.calls:
-        row_bytes = cols // 32 * 34
-        if row_bytes % 16 or table.value % 16:
-            return None
-        probe.calls.append(("drift_row_probe", lib.drift_row_probe,
-                            (table, vocab, row_bytes // 16, ids, count, out, cols * 2 // 16)))
-    return probe
+def row_probes(k: Kernel, lib) -> list:
+    """The gather's own pattern with no decode: each of k's launches (table,
+    ids, out, count, vocab, cols, bad_id) becomes, with the same ids and
+    outputs, a 256-thread block per id reading the whole Q8_0 row the id
+    names and writing the row's BF16 bytes (drift_row_probe), or 1, 2, 4 or
+    8 one-wave blocks per id each reading its slice of the row and writing
+    its slice of the output (drift_wave_row_probe; the gather itself takes 4
+    waves a row). Random rows of a table larger than the cache come from
+    scattered DRAM pages, which the contiguous probes do not measure."""
+    probes = []
+    for slices in (0, 1, 2, 4, 8):
+        what = ("a 256-thread block per id" if slices == 0 else f"{slices} one-wave blocks per id")
+        probe = Kernel(f"row probe of {k.name}", f"rows of the gather's table read at its ids, its output written: "
+                       f"{what}", k.bytes, k.rows, None, k.sets, read_bytes=k.read_bytes)
+        probe.slices = slices
+        for _, _, (table, ids, out, count, vocab, cols, _) in k.calls:
+            row_bytes = cols // 32 * 34
+            if row_bytes % 16 or table.value % 16:
+                return []
+            if slices == 0:
+                probe.calls.append(("drift_row_probe", lib.drift_row_probe,
+                                    (table, vocab, row_bytes // 16, ids, count, out, cols * 2 // 16)))
+            else:
+                probe.calls.append(("drift_wave_row_probe", lib.drift_wave_row_probe,
+                                    (table, vocab, row_bytes // 16, ids, count, out, cols * 2 // 16, slices)))
+        probes.append(probe)
+    return probes
 
 
 def floor_probe(lib) -> Kernel:
@@ -813,8 +832,8 @@ def main():
     rows_probes = {}
     for k in kernels:
         if k.name == "embedding_q8_0_bf16":
-            p = row_probe(k, lib)
-            if p is not None:
+            p = row_probes(k, lib)
+            if p:
                 rows_probes[k.name] = p
     reads = [] if args.only else [read_probe(lib, 1 << 30, 2048, "read_sum_1gib_2048_blocks"),
                                   read_probe(lib, 1 << 30, (1 << 30) // 16 // 1024, "read_sum_1gib_one_pass")]
@@ -829,8 +848,8 @@ def main():
     largest_first = sorted(kernels, key=lambda k: k.bytes, reverse=True)
     wall = time_graphs(largest_first, args.steps, args.warmup)
     time_eager(largest_first, args.steps)
-    time_graphs([p for group in probes.values() for p in group] + list(rows_probes.values()) + reads + floors,
-                args.steps, args.warmup)
+    time_graphs([p for group in probes.values() for p in group] + [p for group in rows_probes.values() for p in group]
+                + reads + floors, args.steps, args.warmup)
     ceilings = {}
     for k in kernels:
         if k.name not in probes:
@@ -839,12 +858,14 @@ def main():
         k.ceiling = best
         gbs = best.bytes / (best.graph_ms * 1e-3) / 1e9
         ceilings[k.name] = {"read_bytes": best.read_bytes, "write_bytes": best.bytes - best.read_bytes,
-                            "chunks_a_lane": best.per_lane, "us": round(best.graph_ms * 1e3, 2),
+                            "probe": best.shape, "chunks_a_lane": best.per_lane, "us": round(best.graph_ms * 1e3, 2),
                             "GB_s": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
-                            "us_by_chunks_a_lane": {p.per_lane: round(p.graph_ms * 1e3, 2) for p in probes[k.name]}}
-    # each kernel against its best probe (and the gather against its row
+                            "us_by_probe": {f"{p.shape} {p.per_lane} a lane": round(p.graph_ms * 1e3, 2)
+                                            for p in probes[k.name]}}
+    # each kernel against its best probe (and the gather against its best row
     # probe) under the same conditions, in alternation
-    groups = [[k, k.ceiling] + ([rows_probes[k.name]] if k.name in rows_probes else []) for k in kernels
+    best_rows = {name: min(group, key=lambda p: p.graph_ms) for name, group in rows_probes.items()}
+    groups = [[k, k.ceiling] + ([best_rows[k.name]] if k.name in best_rows else []) for k in kernels
               if k.ceiling is not None]
     time_matched(groups, args.steps, MATCHED_ROUNDS)
     for group in groups:
@@ -856,10 +877,13 @@ def main():
             matched["row_probe_us"] = round(group[2].matched_ms * 1e3, 2)
             matched["frac_of_row_probe"] = round(group[2].matched_ms / k.matched_ms, 4)
         ceilings[k.name]["matched"] = matched
-    for name, p in rows_probes.items():
+    for name, group in rows_probes.items():
+        p = best_rows[name]
         gbs = p.bytes / (p.graph_ms * 1e-3) / 1e9
         ceilings[name]["row_probe"] = {"us": round(p.graph_ms * 1e3, 2), "GB_s": round(gbs, 1),
-                                       "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "what": p.config}
+                                       "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "what": p.config,
+                                       "us_by_shape": {("block per id" if q.slices == 0 else f"{q.slices} waves per id"):
+                                                       round(q.graph_ms * 1e3, 2) for q in group}}
     for r in reads:
         gbs = r.bytes / (r.graph_ms * 1e-3) / 1e9
         ceilings[r.name] = {"bytes": r.bytes, "us": round(r.graph_ms * 1e3, 2), "GB_s": round(gbs, 1),
@@ -919,11 +943,17 @@ def main():
     dominant = max(kernels, key=lambda k: k.graph_ms)
     dom_avg = dominant.graph_ms
     achieved = dominant.bytes / (dom_avg * 1e-3) / 1e9
-    traffic = None
+    # HBM bytes per launch are not measured in this run (counters need a
+    # profiler pass of their own): they come from the committed counter
+    # passes, and the line says which
+    traffic = traffic_source = None
     traffic_file = os.path.join(ROOT, "profiles", "traffic.json")
     if os.path.exists(traffic_file):
         with open(traffic_file) as f:
-            traffic = json.load(f).get(dominant.name)
+            counted = json.load(f)
+        traffic = counted.get(dominant.name)
+        traffic_source = (f"profiles/traffic.json: {counted.get('_how', 'rocprofv3 FETCH_SIZE and WRITE_SIZE passes')}"
+                          f" ({counted.get('_date', 'date not recorded')}), not this run")
     line = {
         "metric": "achieved HBM GB/s and % of MI355X peak per fused kernel; rows/sec at 1 GPU",
         "value": round(step_bytes / (ms_per_step * 1e-3) / 1e9, 1),
@@ -955,6 +985,7 @@ def main():
         "roofline": {
             "kernel": dominant.name, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
             "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+            "traffic_source": traffic_source,
             "algorithmic_bytes_per_launch": dominant.bytes, "avg_launch_us": round(dom_avg * 1e3, 2),
         },
     }

@@ -79,6 +79,8 @@ SIGNATURES = {
     "drift_read_sum_f32x4": (_I32, [_P, _I64, _P, _I32, _P]),
     "drift_stream_mix": (_I32, [_P, _I64, _P, _I64, _I32, _P]),
     "drift_row_probe": (_I32, [_P, _I64, _I32, _P, _I64, _P, _I32, _P]),
+    "drift_wave_copy": (_I32, [_P, _I64, _P, _I64, _I32, _P]),
+    "drift_wave_row_probe": (_I32, [_P, _I64, _I32, _P, _I64, _P, _I32, _I32, _P]),
 }
 
 ABI_VERSION = 8

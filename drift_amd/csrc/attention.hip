@@ -653,7 +653,9 @@ int qk_norm_rope(const char* entry, const T* q, const T* k, T* q_out, T* k_out, 
   a.eps = eps;
   a.offset = offset;
   a.q_stride = dim;
-  const bool aligned = (!q || (aligned16(q) && aligned16(q_out))) && (!k || (aligned16(k) && aligned16(k_out)));
+  // the fast body reads the norm weights as 16-byte loads too
+  const bool aligned = (!q || (aligned16(q) && aligned16(q_out) && aligned16(q_weight))) &&
+                       (!k || (aligned16(k) && aligned16(k_out) && aligned16(k_weight)));
   return qk_launch<T, false>(entry, q, k, q_out, k_out, q_weight, k_weight, positions, a, Extras<T>{}, aligned,
                              (hipStream_t)stream);
 }
@@ -691,8 +693,8 @@ int attention_inputs(const char* entry, const T* query_and_gate, const T* k, con
   a.offset = offset;
   a.q_stride = gate ? 2 * (int64_t)dim : dim;
   const Extras<T> e{gate, v, keys, values, page_table, cache_pages, page_size, start, bad_page, 0};
-  const bool aligned = (!query_and_gate || (aligned16(query_and_gate) && aligned16(queries))) &&
-                       (!gate || aligned16(gate)) && (!k || (aligned16(k) && aligned16(v))) &&
+  const bool aligned = (!query_and_gate || (aligned16(query_and_gate) && aligned16(queries) && aligned16(q_norm))) &&
+                       (!gate || aligned16(gate)) && (!k || (aligned16(k) && aligned16(v) && aligned16(k_norm))) &&
                        (!keys || (aligned16(keys) && aligned16(values)));
   return qk_launch<T, true>(entry, query_and_gate, k, queries, nullptr, q_norm, k_norm, positions, a, e, aligned,
                             (hipStream_t)stream);

@@ -24,7 +24,21 @@
 // lane's stores carrying the XOR of what it read. Rows drawn at random from a
 // table larger than the cache are read from scattered DRAM pages, which a
 // contiguous stream does not measure.
+//
+// wave_copy and wave_row_probe are the same two patterns in the shape the
+// fused kernels take: one-wave blocks, each wave reading its share of the
+// input and then writing its share of the output, every store carrying the
+// fold of what its lane read (so, as in a kernel, a wave's stores wait for
+// its loads). wave_copy spreads the reads and the writes evenly over the
+// waves; wave_row_probe gives each id `slices` waves, wave s of an id reading
+// slice s of the row and writing slice s of the output row. At the sizes of
+// the prefill shapes one-wave blocks stream faster than 256-thread blocks, so
+// these are the tighter ceilings there.
 #include "common.hpp"
+
+#include <algorithm>
+#include <climits>
+#include <type_traits>
 
 namespace drift {
 namespace {
@@ -105,6 +119,101 @@ __global__ void __launch_bounds__(256) row_probe_kernel(const uint4* table, int6
   }
 }
 
+// One wave's part of a one-wave-block probe: lane l reads chunks r0 + l +
+// 64 k (k < R) below r1, all in flight together, then writes chunks w0 + l +
+// 64 k (k < W) below w1, each holding the XOR of what the lane read with its
+// first word XORed with the chunk's index in [w0, w1).
+template <int R, int W>
+__device__ __forceinline__ void wave_part(const uint4* src, int64_t r0, int64_t r1, uint4* dst, int64_t w0,
+                                          int64_t w1) {
+  const int lane = threadIdx.x;
+  uint4 v[R];
+#pragma unroll
+  for (int k = 0; k < R; ++k) {
+    const int64_t i = r0 + lane + (int64_t)k * kWave;
+    v[k] = i < r1 ? stream_load(src + i) : make_uint4(0, 0, 0, 0);
+  }
+  uint4 acc = v[0];
+#pragma unroll
+  for (int k = 1; k < R; ++k) acc = make_uint4(acc.x ^ v[k].x, acc.y ^ v[k].y, acc.z ^ v[k].z, acc.w ^ v[k].w);
+#pragma unroll
+  for (int k = 0; k < W; ++k) {
+    const int64_t j = w0 + lane + (int64_t)k * kWave;
+    if (j < w1) {
+      const u32x4 q = {acc.x ^ (uint32_t)(j - w0), acc.y, acc.z, acc.w};
+      __builtin_nontemporal_store(q, reinterpret_cast<u32x4*>(dst + j));
+    }
+  }
+}
+
+// wave b reads chunks [b rpw, (b + 1) rpw) and writes [b wpw, (b + 1) wpw),
+// each cut at the end of its tensor
+template <int R, int W>
+__global__ void __launch_bounds__(kWave) wave_copy_kernel(const uint4* src, int64_t read_chunks, uint4* dst,
+                                                          int64_t write_chunks, int rpw, int wpw) {
+  const int64_t b = blockIdx.x;
+  wave_part<R, W>(src, b * rpw, min(b * rpw + rpw, read_chunks), dst, b * wpw, min(b * wpw + wpw, write_chunks));
+}
+
+// wave b takes slice s = b % slices of id t = b / slices (clamped into the
+// table): row chunks [s rs, (s + 1) rs) and output chunks [s os, (s + 1) os)
+template <int R, int W>
+__global__ void __launch_bounds__(kWave) wave_row_kernel(const uint4* table, int64_t rows, int row_chunks,
+                                                         const int32_t* ids, uint4* out, int out_chunks, uint32_t slices,
+                                                         int rs, int os) {
+  const uint32_t t = blockIdx.x / slices, s = blockIdx.x - t * slices;
+  const int64_t id = min(max((int64_t)ids[t], (int64_t)0), rows - 1);
+  const uint4* row = table + id * row_chunks;
+  uint4* target = out + (int64_t)t * out_chunks;
+  wave_part<R, W>(row, (int64_t)s * rs, min((int64_t)(s + 1) * rs, (int64_t)row_chunks), target, (int64_t)s * os,
+                  min((int64_t)(s + 1) * os, (int64_t)out_chunks));
+}
+
+// the smallest of 1, 2, 4, 8 chunks a lane that covers `chunks` in a wave
+// (0 if none does)
+inline int lanes_cover(int64_t chunks) {
+  for (int per = 1; per <= 8; per *= 2)
+    if (chunks <= (int64_t)per * kWave) return per;
+  return 0;
+}
+
+template <template <int, int> class Launch, typename... Args>
+void launch_rw(int r, int w, Args... args) {
+  auto by_w = [&](auto rc) {
+    constexpr int R = decltype(rc)::value;
+    switch (w) {
+      case 1: Launch<R, 1>::go(args...); break;
+      case 2: Launch<R, 2>::go(args...); break;
+      case 4: Launch<R, 4>::go(args...); break;
+      default: Launch<R, 8>::go(args...); break;
+    }
+  };
+  switch (r) {
+    case 1: by_w(std::integral_constant<int, 1>{}); break;
+    case 2: by_w(std::integral_constant<int, 2>{}); break;
+    case 4: by_w(std::integral_constant<int, 4>{}); break;
+    default: by_w(std::integral_constant<int, 8>{}); break;
+  }
+}
+
+template <int R, int W>
+struct WaveCopyLaunch {
+  static void go(int64_t waves, hipStream_t s, const uint4* in, int64_t reads, uint4* out, int64_t writes, int rpw,
+                 int wpw) {
+    hipLaunchKernelGGL((wave_copy_kernel<R, W>), dim3((unsigned)waves), dim3(kWave), 0, s, in, reads, out, writes,
+                       rpw, wpw);
+  }
+};
+
+template <int R, int W>
+struct WaveRowLaunch {
+  static void go(int64_t waves, hipStream_t s, const uint4* table, int64_t rows, int row_chunks, const int32_t* ids,
+                 uint4* out, int out_chunks, int slices, int rs, int os) {
+    hipLaunchKernelGGL((wave_row_kernel<R, W>), dim3((unsigned)waves), dim3(kWave), 0, s, table, rows, row_chunks,
+                       ids, out, out_chunks, (uint32_t)slices, rs, os);
+  }
+};
+
 }  // namespace
 }  // namespace drift
 
@@ -169,5 +278,44 @@ extern "C" int drift_row_probe(const void* table, int64_t rows, int32_t row_chun
     hipLaunchKernelGGL(row_probe_kernel<1>, grid, dim3(256), 0, s, in, rows, row_chunks, ids, o, out_chunks);
   else
     hipLaunchKernelGGL(row_probe_kernel<2>, grid, dim3(256), 0, s, in, rows, row_chunks, ids, o, out_chunks);
+  return launched(entry);
+}
+
+extern "C" int drift_wave_copy(const void* src, int64_t read_chunks, void* dst, int64_t write_chunks,
+                               int32_t per_lane, void* stream) {
+  const char* entry = "drift_wave_copy";
+  clear_error();
+  if (read_chunks < 0 || write_chunks < 1 || lanes_cover((int64_t)per_lane * kWave) != per_lane)
+    return refuse("%s: %lld chunks read, %lld written, %d a lane (at least one written; 1, 2, 4 or 8 a lane)", entry,
+                  (long long)read_chunks, (long long)write_chunks, per_lane);
+  if ((read_chunks > 0 && !src) || !dst) return refuse("%s: null src or dst", entry);
+  if ((read_chunks > 0 && !aligned16(src)) || !aligned16(dst)) return refuse("%s: src or dst is not 16-byte aligned", entry);
+  const int64_t waves = std::max(ceil_div(read_chunks, (int64_t)per_lane * kWave),
+                                 ceil_div(write_chunks, (int64_t)per_lane * kWave));
+  if (waves > INT32_MAX) return refuse("%s: %lld chunks", entry, (long long)std::max(read_chunks, write_chunks));
+  // a wave's share, ceil(chunks / waves), is at most per_lane * 64
+  const int64_t rpw = ceil_div(read_chunks, waves), wpw = ceil_div(write_chunks, waves);
+  const int r = std::max(lanes_cover(rpw), 1), w = lanes_cover(wpw);
+  launch_rw<WaveCopyLaunch>(r, w, waves, (hipStream_t)stream, static_cast<const uint4*>(src), read_chunks,
+                            static_cast<uint4*>(dst), write_chunks, (int)rpw, (int)wpw);
+  return launched(entry);
+}
+
+extern "C" int drift_wave_row_probe(const void* table, int64_t rows, int32_t row_chunks, const int32_t* ids,
+                                    int64_t count, void* out, int32_t out_chunks, int32_t slices, void* stream) {
+  const char* entry = "drift_wave_row_probe";
+  clear_error();
+  if (rows < 1 || row_chunks < 1 || count < 0 || out_chunks < 1 || slices < 1 ||
+      ceil_div(row_chunks, slices) > 8 * kWave || ceil_div(out_chunks, slices) > 8 * kWave)
+    return refuse("%s: %lld ids into %lld rows of %d chunks, %d chunks out each, %d waves a row (at most 512 chunks "
+                  "a wave each way)", entry, (long long)count, (long long)rows, row_chunks, out_chunks, slices);
+  if (count == 0) return 0;
+  if (!table || !ids || !out) return refuse("%s: null table, ids or out", entry);
+  if (!aligned16(table) || !aligned16(out)) return refuse("%s: table or out is not 16-byte aligned", entry);
+  if (count > INT32_MAX / slices) return refuse("%s: %lld ids of %d waves", entry, (long long)count, slices);
+  const int rs = (int)ceil_div(row_chunks, slices), os = (int)ceil_div(out_chunks, slices);
+  launch_rw<WaveRowLaunch>(lanes_cover(rs), lanes_cover(os), count * slices, (hipStream_t)stream,
+                           static_cast<const uint4*>(table), rows, (int)row_chunks, ids, static_cast<uint4*>(out),
+                           (int)out_chunks, (int)slices, rs, os);
   return launched(entry);
 }

@@ -11,10 +11,16 @@
 //   gelu_tanh(v) = v/2 (1 + tanh u) with 1 + tanh u = 2/(1 + e^-2u) or
 //                  2e^2u/(1 + e^2u)
 //   gelu_erf(v)  = v/2 erfc(-v/sqrt2)
-// and, where the reference's own double result is quantized (1 + tanh u and
+// Where the reference's own double result is quantized (1 + tanh u and
 // 1 + erf x below 2^-29 hold a whole number of 2^-53 steps, the spacing of
-// doubles just above -1), the same quantization is applied, so the results
-// agree with the reference there too. F32 outputs use the accurate library
+// doubles just above -1, so far enough into the tail one step is more than
+// 1e-5 of the value), F32 outputs take the reference's steps in double
+// instead: 1 + tanh u as the C library's tanh makes it (fdlibm's s_tanh.c,
+// 1 - 2/(expm1(2|u|) + 2) for 1 <= |u| < 22, -1 beyond; equal to glibc's
+// 1 + tanh(u) on every one of 2e7 sampled u in [-22.5, -1]), and 1 + erf x as
+// CpuOps.erf makes it (ops/CpuOps.scala:26-50: 1 - (1 - E), E from the
+// 60-level continued fraction). BF16 outputs round the float sum to the same
+// step instead, well within their ulp. F32 outputs use the accurate library
 // exp and IEEE division. BF16 outputs use the hardware exp2 and reciprocal
 // (v_exp_f32, v_rcp_f32: about 1e-6 relative, far below a bf16 ulp, and BF16
 // output is all the precision they feed), with GELU-tanh's sigmoid form
@@ -32,13 +38,6 @@ __device__ __forceinline__ float divide(float a, float b) {
     return a / b;
   else
     return a * __builtin_amdgcn_rcpf(b);
-}
-
-// A double's 1 + t for t in (-1, -1/2]: a whole number of 2^-53 steps. t here
-// is that sum computed in float; below 2^-29 it is rounded to the step.
-__device__ __forceinline__ float quantize_2m53(float t) {
-  const float steps = rintf(t * 0x1p53f);
-  return t < 0x1p-29f ? steps * 0x1p-53f : t;
 }
 
 template <bool ACCURATE>
@@ -76,6 +75,36 @@ __device__ __forceinline__ void gelu_tanh_fast(float (&v)[M]) {
   for (int j = 0; j < M; ++j) v[j] *= h[j];
 }
 
+// The reference's double constants: sqrt(2 / pi), sqrt(pi) and sqrt(2) as
+// math.sqrt rounds them.
+constexpr double kSqrt2OverPi = 0x1.9884533d43651p-1;
+constexpr double kSqrtPi = 0x1.c5bf891b4ef6ap+0;
+constexpr double kSqrt2 = 0x1.6a09e667f3bcdp+0;
+
+// GELU-tanh of an F32 value whose 1 + tanh u lies in the quantized tail, the
+// reference's double arithmetic step by step (ops/CpuNormalisation.scala:14):
+// u = sqrt(2/pi) (v + 0.044715 v^3); 1 + tanh u for u <= -1 from the C
+// library's formula; 0.5 v (1 + tanh u).
+__device__ __attribute__((noinline)) float gelu_tanh_tail(float value) {
+  const double v = value;
+  const double u = kSqrt2OverPi * (v + 0.044715 * v * v * v);
+  const double a = -2.0 * u;  // 2|u|: the tail has u < -10
+  const double t = a >= 44.0 ? 0.0 : 1.0 - (1.0 - 2.0 / (expm1(a) + 2.0));
+  return (float)(0.5 * v * t);
+}
+
+// GELU-erf of an F32 value whose 1 + erf x lies in the quantized tail (x =
+// v / sqrt 2 at or below -2.5): CpuOps.erf's continued fraction for -x, then
+// 1 + erf x = 1 - (1 - E) as the reference's double sums make it.
+__device__ __attribute__((noinline)) float gelu_erf_tail(float value) {
+  const double v = value;
+  const double x = -(v / kSqrt2);
+  double fraction = 0.0;
+  for (int n = 60; n >= 1; --n) fraction = (n / 2.0) / (x + fraction);
+  const double e = exp(-x * x) / kSqrtPi / (x + fraction);
+  return (float)(0.5 * v * (1.0 - (1.0 - e)));
+}
+
 template <bool ACCURATE>
 __device__ __forceinline__ float activate(int kind, float v) {
   switch (kind) {
@@ -90,11 +119,11 @@ __device__ __forceinline__ float activate(int kind, float v) {
       const float u = 0.7978845608028654f * (v + 0.044715f * v * v * v);
       const float e = expf(-2.0f * fabsf(u));
       const float t = (u >= 0.0f ? 2.0f : 2.0f * e) / (1.0f + e);  // 1 + tanh(u)
-      return 0.5f * v * quantize_2m53(t);
+      return t < 0x1p-29f ? gelu_tanh_tail(v) : 0.5f * v * t;
     }
     case DRIFT_GELU_ERF: {
       const float t = erfcf(-v * 0.70710678118654752f);  // 1 + erf(v / sqrt 2)
-      return 0.5f * v * quantize_2m53(t);
+      return t < 0x1p-29f ? gelu_erf_tail(v) : 0.5f * v * t;
     }
     case DRIFT_SIGMOID:
       return sigmoid_of<ACCURATE>(v);

@@ -282,7 +282,7 @@ class _Reader:
             # an offset before the data section would place the tensor over
             # the header (the reference's bounds-checked slice refuses it)
             if offset < 0:
-                self.fail(f"{name} starts {-offset} bytes before the data section")
+                self.fail(f"{name} starts at offset {offset}, before the data section")
             infos.append((name, dims, type_id, offset))
         data_start = (self.position + alignment - 1) // alignment * alignment
         data_bytes = self.size - data_start
@@ -298,6 +298,8 @@ class _Reader:
                 self.fail(f"{name}: rows of {dims[0]} are not whole {t.name} blocks")
             if offset % alignment != 0:
                 self.fail(f"{name} is not aligned to {alignment}")
+            if offset > data_bytes:
+                self.fail(f"{name} runs past the end of the file")
             tensor = StoredTensor(name, t, tuple(reversed(dims)), data_start + offset)
             try:
                 size = tensor.byteSize

@@ -199,7 +199,8 @@ class Reader {
       info.offset = take<int64_t>();
       // an offset before the data section would place the tensor over the
       // header (the reference's bounds-checked slice refuses it when read)
-      if (info.offset < 0) fail(text(info.name, " starts ", -info.offset, " bytes before the data section"));
+      // (printed as it is: negating INT64_MIN would overflow)
+      if (info.offset < 0) fail(text(info.name, " starts at offset ", info.offset, ", before the data section"));
       infos.push_back(std::move(info));
     }
     const int64_t alignment = f.alignment_;
@@ -217,6 +218,9 @@ class Reader {
       if (!info.dims.empty() && info.dims[0] % t->values != 0)
         fail(text(info.name, ": rows of ", info.dims[0], " are not whole ", t->name, " blocks"));
       if (info.offset % alignment != 0) fail(text(info.name, " is not aligned to ", alignment));
+      // refused before data_start + offset is formed, which an offset near
+      // 2^63 would overflow
+      if (info.offset > data_bytes) fail(info.name + " runs past the end of the file");
       StoredTensor tensor{info.name, t, std::vector<int64_t>(info.dims.rbegin(), info.dims.rend()),
                           data_start + info.offset};
       int64_t size = 0;
@@ -225,7 +229,7 @@ class Reader {
       } catch (const FormatError& e) {
         fail(e.what());
       }
-      if (info.offset > data_bytes || size > data_bytes - info.offset) fail(info.name + " runs past the end of the file");
+      if (size > data_bytes - info.offset) fail(info.name + " runs past the end of the file");
       described[info.name] = tensor;
     }
     // Gguf.checkSpans (Gguf.scala:262-285): each tensor's byte size and the

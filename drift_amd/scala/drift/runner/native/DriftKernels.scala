@@ -101,6 +101,8 @@ final class DriftKernels(path: Path) {
   val readSumF32x4 = bind("drift_read_sum_f32x4", P, JAVA_LONG, P, JAVA_INT, P)
   val streamMix = bind("drift_stream_mix", P, JAVA_LONG, P, JAVA_LONG, JAVA_INT, P)
   val rowProbe = bind("drift_row_probe", P, JAVA_LONG, JAVA_INT, P, JAVA_LONG, P, JAVA_INT, P)
+  val waveCopy = bind("drift_wave_copy", P, JAVA_LONG, P, JAVA_LONG, JAVA_INT, P)
+  val waveRowProbe = bind("drift_wave_row_probe", P, JAVA_LONG, JAVA_INT, P, JAVA_LONG, P, JAVA_INT, JAVA_INT, P)
 
   /** A downcall's result: a nonzero code becomes a HipException carrying the
     * library's reason (as HipRuntime.check does, native/HipRuntime.scala:123-130).
@@ -120,6 +122,31 @@ object DriftKernels {
 
   /** `DRIFT_ABI_VERSION` of the header these bindings repeat. */
   val AbiVersion = 8
+
+  /** Where the runner's build puts the library: the resource
+    * `lib/libdrift_kernels.so` of the runner's jar (the `driftKernels` task
+    * of drift_amd/scala/build.mill.drift, beside the `kernels` task's code
+    * objects).
+    */
+  val Resource = "/lib/libdrift_kernels.so"
+
+  /** The library the runner loads: the file `-Ddrift.kernels=<path>` names,
+    * else the jar's resource, copied to a temporary file (a shared library
+    * is mapped from a file, not from a jar entry) that is removed at exit.
+    */
+  def default(): DriftKernels =
+    sys.props.get("drift.kernels").map(_.trim).filter(_.nonEmpty) match {
+      case Some(path) => new DriftKernels(Path.of(path))
+      case None =>
+        val stream = Option(classOf[DriftKernels].getResourceAsStream(Resource)).getOrElse(
+          throw new IllegalStateException(s"$Resource is not built: build the runner with the driftKernels task")
+        )
+        val file = java.nio.file.Files.createTempFile("libdrift_kernels", ".so")
+        file.toFile.deleteOnExit()
+        try java.nio.file.Files.copy(stream, file, java.nio.file.StandardCopyOption.REPLACE_EXISTING)
+        finally stream.close()
+        new DriftKernels(file)
+    }
 
   /** An entry point's F32 and BF16 forms. The header's enumerations are the
     * runner's own codes: `Activation.code`, `RopeLayout.code`,

@@ -29,11 +29,21 @@ private[ops] trait DriftBase extends HipBase {
   /** The default stream, where the runner launches everything. */
   protected val DefaultStream: MemorySegment = MemorySegment.NULL
 
-  /** One downcall: counted as a launch, then made, its code checked. */
+  /** One downcall: counted as a launch, then made, its code checked. With
+    * `DRIFT_HIP_TRACE` set it is timed as `HipRuntime.launch` times a kernel
+    * (native/HipRuntime.scala:318,358-362): from before the call until the
+    * device has finished it, recorded under the entry point's name in the
+    * per-kernel table printed at exit.
+    */
   protected def downcall(name: => String)(call: => Int): Unit = {
     deviceWrites += 1
     onWork()
-    drift.check(name, call)
+    if (HipRuntime.Trace.on) {
+      val from = System.nanoTime()
+      drift.check(name, call)
+      hip.synchronize()
+      HipRuntime.Trace.record(name, System.nanoTime() - from)
+    } else drift.check(name, call)
   }
 
   /** Whether `tensor` takes an entry point's BF16 form. */

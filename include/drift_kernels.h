@@ -448,6 +448,25 @@ int drift_stream_mix(const void* src, int64_t read_chunks, void* dst, int64_t wr
  * counterpart in the reference. */
 int drift_row_probe(const void* table, int64_t rows, int32_t row_chunks, const int32_t* ids, int64_t count, void* out,
                     int32_t out_chunks, void* stream);
+/* drift_wave_copy: a fused kernel's read/write mix in its own shape, for its
+ * ceiling: one-wave blocks, wave b reading chunks [b r, (b + 1) r) of src and
+ * then writing chunks [b w, (b + 1) w) of dst (r and w the even shares of
+ * read_chunks and write_chunks over max(read_chunks, write_chunks) / (64
+ * per_lane) waves, rounded up; per_lane 1, 2, 4 or 8; at least one chunk
+ * written). Each lane's written chunks hold the XOR of the chunks it read,
+ * the first word also XORed with the chunk's place in the wave's share; src
+ * and dst 16-byte aligned. No counterpart in the reference.
+ * drift_wave_row_probe: a gather's bytes in the gather's own shape: `slices`
+ * one-wave blocks per id, wave s of id t reading chunks [s r, (s + 1) r) of
+ * table row ids[t] (clamped into the table; r = row_chunks / slices rounded
+ * up, at most 512) and writing chunks [s o, (s + 1) o) of out row t (o =
+ * out_chunks / slices rounded up, at most 512), each lane's chunks holding
+ * the XOR of what it read as in drift_wave_copy. No counterpart in the
+ * reference. */
+int drift_wave_copy(const void* src, int64_t read_chunks, void* dst, int64_t write_chunks, int32_t per_lane,
+                    void* stream);
+int drift_wave_row_probe(const void* table, int64_t rows, int32_t row_chunks, const int32_t* ids, int64_t count,
+                         void* out, int32_t out_chunks, int32_t slices, void* stream);
 
 #ifdef __cplusplus
 }

@@ -165,3 +165,19 @@ def test_probes_refuse_bad_geometry(lib):
     assert "0 rows" in refused(lib, "drift_row_probe", p, 0, 16, p, 4, p, 8, NULL)
     assert "null" in refused(lib, "drift_row_probe", p, 10, 16, NULL, 4, p, 8, NULL)
     assert "not 16-byte aligned" in refused(lib, "drift_row_probe", p, 10, 16, p, 4, ctypes.c_void_p(8), 8, NULL)
+
+
+def test_wave_probes_refuse_bad_geometry(lib):
+    p = ctypes.c_void_p(16)
+    assert "at least one written" in refused(lib, "drift_wave_copy", p, 10, p, 0, 1, NULL)
+    assert "3 a lane" in refused(lib, "drift_wave_copy", p, 10, p, 10, 3, NULL)
+    assert "16 a lane" in refused(lib, "drift_wave_copy", p, 10, p, 10, 16, NULL)
+    assert "null" in refused(lib, "drift_wave_copy", NULL, 10, p, 10, 1, NULL)
+    assert "not 16-byte aligned" in refused(lib, "drift_wave_copy", p, 10, ctypes.c_void_p(8), 10, 1, NULL)
+    assert "at most 512 chunks" in refused(lib, "drift_wave_row_probe", p, 10, 1025, p, 4, p, 8, 2, NULL)
+    assert "at most 512 chunks" in refused(lib, "drift_wave_row_probe", p, 10, 16, p, 4, p, 600, 1, NULL)
+    assert "0 waves a row" in refused(lib, "drift_wave_row_probe", p, 10, 16, p, 4, p, 8, 0, NULL)
+    assert "null" in refused(lib, "drift_wave_row_probe", p, 10, 16, NULL, 4, p, 8, 1, NULL)
+    assert "not 16-byte aligned" in refused(lib, "drift_wave_row_probe", p, 10, 16, p, 4, ctypes.c_void_p(8), 8, 1,
+                                            NULL)
+    assert lib.drift_wave_row_probe(NULL, 10, 16, NULL, 0, NULL, 8, 1, NULL) == 0

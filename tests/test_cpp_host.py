@@ -96,7 +96,7 @@ def test_the_gguf_readers_agree(tmp_path):
     assert result.returncode == 0, result.stderr
     want = [line for path in files for line in python_summary(path)]
     assert result.stdout.splitlines() == want
-    assert sum(line.startswith("refused ") for line in want) == 17
+    assert sum(line.startswith("refused ") for line in want) == 20
 
 
 def fnv1a(data: bytes) -> int:

@@ -98,14 +98,18 @@ def test_refusals_of_the_tensors():
 
 def crafted_files():
     """Files whose tensor records point outside the data or overflow: a
-    negative offset (over the header) and dimensions whose product passes
-    2^63, each with the message both readers give."""
+    negative offset (over the header, down to -2^63), an aligned offset just
+    below 2^63 (data start + offset would overflow an int64) and dimensions
+    whose product passes 2^63, each with the message both readers give."""
     q8 = o.quant_table("Q8_0", 2, 64, np.random.default_rng(1)).tobytes()
     rocm = o.quant_table("Q4_0_ROCMFP4", 1, 64, np.random.default_rng(2)).tobytes()
     big = [64] + [1 << 10] * 6 + [1 << 4]  # 2^6 * 2^60 * 2^4 = 2^70 values, each dimension within the file's size
     return [
-        (one_tensor(8, [64, 2], -6528, q8), "t starts 6528 bytes before the data section"),
-        (one_tensor(100, [64, 1], -32, rocm), "t starts 32 bytes before the data section"),
+        (one_tensor(8, [64, 2], -6528, q8), "t starts at offset -6528, before the data section"),
+        (one_tensor(100, [64, 1], -32, rocm), "t starts at offset -32, before the data section"),
+        (one_tensor(8, [64, 2], -(1 << 63), q8), "t starts at offset -9223372036854775808, before the data section"),
+        (one_tensor(8, [64, 2], ((1 << 63) - 1) // 32 * 32, q8), "t runs past the end of the file"),
+        (one_tensor(8, [64, 2], ((1 << 63) - 1) // 32 * 32 - 32 * 1024, q8), "t runs past the end of the file"),
         (one_tensor(8, big, 0, q8 + bytes(1 << 16)), r"t of \[16, 1024, 1024, 1024, 1024, 1024, 1024, 64\] has "
                                                     r"more than 2\^63 elements"),
         # 2^61 F32 values fit an int64, their 2^63 bytes do not

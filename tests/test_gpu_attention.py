@@ -112,7 +112,13 @@ REFERENCE_ROPE = d.Rope(1e7, 64, d.RopeLayout.Neox, d.RopeSections.Interleaved(1
 QWEN3_ROPE = d.Rope(1e6, 128, d.RopeLayout.Neox, d.RopeSections.Single())
 
 
-def run_attention_inputs(hip, dtype, t, heads, kv, dim, rope, start, table, pages, gated, seed, offset=0.0):
+def shifted(values: np.ndarray, shift: int) -> torch.Tensor:
+    """values on the device, starting `shift` floats into their buffer."""
+    return dev_f32(np.concatenate([np.full(shift, 7.0, np.float32), values]))[shift:]
+
+
+def run_attention_inputs(hip, dtype, t, heads, kv, dim, rope, start, table, pages, gated, seed, offset=0.0,
+                         weight_shift=0):
     rng = np.random.default_rng(seed)
     width = 2 * dim if gated else dim
     qg = (2 * rng.standard_normal((t, heads, width))).astype(np.float32)
@@ -124,7 +130,7 @@ def run_attention_inputs(hip, dtype, t, heads, kv, dim, rope, start, table, page
     positions = np.array([start + i % t + i // t for i in range(count * t)], np.int32)
     positions = positions.reshape(count, t) if count > 1 else positions
     c, keys0, values0 = cache(pages, kv, dim, seed + 1)
-    norms = d.QueryKeyNorms(dev_f32(qw), dev_f32(kw), 1e-6, offset, rope)
+    norms = d.QueryKeyNorms(shifted(qw, weight_shift), shifted(kw, 2 * weight_shift), 1e-6, offset, rope)
     bf = dtype == "bf16"
     if bf:
         qgb, kb, vb = bf16_input(qg), bf16_input(k), bf16_input(v)
@@ -234,3 +240,15 @@ def test_attention_inputs_flag_a_page_outside_the_cache(hip):
     assert int(bad.item()) == 1
     assert_bits(keys0, host_bits(c.keys), what="keys untouched")
     assert_bits(values0, host_bits(c.values), what="values untouched")
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("gated", [True, False])
+def test_attention_inputs_with_weights_off_a_16_byte_boundary(hip, dtype, gated):
+    # norm weights 4 and 8 bytes into their buffers: the fast body reads
+    # weights as 16-byte loads, so these take the general kernel
+    t, start = 21, 5
+    step(f"attentionInputs {dtype} Qwen3 heads, norm weights off a 16-byte boundary, gated {gated}")
+    pages = -(-(start + t) // PAGE) + 1
+    table = np.random.default_rng(9).permutation(pages).astype(np.int32)
+    run_attention_inputs(hip, dtype, t, 32, 8, 128, QWEN3_ROPE, start, table, pages, gated, 170, weight_shift=1)

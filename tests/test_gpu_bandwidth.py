@@ -75,3 +75,68 @@ def test_row_probe_writes_what_each_row_holds(rows, row_chunks, count, out_chunk
         want[t] = folded[j % 256]
         want[t, :, 0] ^= j.astype(np.uint32)
     assert np.array_equal(got, want)
+
+
+def _fold_rows(chunks: np.ndarray, r0: int, r1: int) -> np.ndarray:
+    """What wave_part leaves in each lane: the XOR of chunks r0 + lane + 64 k below r1."""
+    folded = np.zeros((64, 4), dtype=np.uint32)
+    for i in range(r0, r1):
+        folded[(i - r0) % 64] ^= chunks[i]
+    return folded
+
+
+def _wave_out(folded: np.ndarray, w0: int, w1: int) -> np.ndarray:
+    """Chunks [w0, w1) as a wave writes them: lane (j - w0) % 64's fold, word 0 XOR (j - w0)."""
+    j = np.arange(w1 - w0)
+    out = folded[j % 64].copy()
+    out[:, 0] ^= j.astype(np.uint32)
+    return out
+
+
+@pytest.mark.parametrize("reads,writes,per", [(1, 1, 1), (1000, 3000, 2), (35651, 67108, 8), (0, 513, 1),
+                                              (2, 7000, 2), (9000, 5, 4), (4096, 4096, 4)])
+def test_wave_copy_folds_each_waves_reads_into_its_writes(reads, writes, per):
+    # wave b reads [b r, (b + 1) r) and writes [b w, (b + 1) w), r and w the
+    # even shares over max(reads, writes) / (64 per) waves, rounded up
+    step(f"wave_copy {reads} chunks read, {writes} written, {per} a lane")
+    rng = np.random.default_rng(reads + 7 * writes)
+    chunks = rng.integers(0, 2**32, (max(reads, 1), 4), dtype=np.uint64).astype(np.uint32)
+    src = torch.from_numpy(chunks.view(np.int32)).to(DEV)
+    dst = torch.zeros((writes, 4), dtype=torch.int32, device=DEV)
+    _lib.call("drift_wave_copy", ctypes.c_void_p(src.data_ptr()), reads, ctypes.c_void_p(dst.data_ptr()), writes,
+              per, None)
+    got = dst.cpu().numpy().view(np.uint32)
+    waves = max(-(-reads // (64 * per)), -(-writes // (64 * per)))
+    r, w = -(-reads // waves), -(-writes // waves)
+    want = np.zeros((writes, 4), dtype=np.uint32)
+    for b in range(waves):
+        w0, w1 = b * w, min(b * w + w, writes)
+        if w0 < w1:
+            want[w0:w1] = _wave_out(_fold_rows(chunks, b * r, min(b * r + r, reads)), w0, w1)
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("rows,row_chunks,count,out_chunks,slices", [(5, 1, 3, 1, 1), (40, 272, 17, 512, 4),
+                                                                     (9, 256, 8, 300, 2), (300, 512, 64, 1000, 2),
+                                                                     (3, 100, 1, 3, 3), (50, 272, 33, 512, 1)])
+def test_wave_row_probe_folds_each_slice(rows, row_chunks, count, out_chunks, slices):
+    # wave s of id t folds row chunks [s r, (s + 1) r) of row ids[t] (clamped)
+    # into output chunks [s o, (s + 1) o) of row t
+    step(f"wave_row_probe {count} ids into {rows} rows of {row_chunks} chunks, {out_chunks} out, {slices} waves a row")
+    rng = np.random.default_rng(rows + row_chunks + slices)
+    table = rng.integers(0, 2**32, (rows, row_chunks, 4), dtype=np.uint64).astype(np.uint32)
+    ids = rng.integers(-2, rows + 2, count).astype(np.int32)
+    dt = torch.from_numpy(table.view(np.int32)).to(DEV)
+    di = torch.from_numpy(ids).to(DEV)
+    out = torch.zeros((count, out_chunks, 4), dtype=torch.int32, device=DEV)
+    _lib.call("drift_wave_row_probe", ctypes.c_void_p(dt.data_ptr()), rows, row_chunks, ctypes.c_void_p(di.data_ptr()),
+              count, ctypes.c_void_p(out.data_ptr()), out_chunks, slices, None)
+    got = out.cpu().numpy().view(np.uint32)
+    r, o = -(-row_chunks // slices), -(-out_chunks // slices)
+    want = np.zeros((count, out_chunks, 4), dtype=np.uint32)
+    for t, id_ in enumerate(np.clip(ids, 0, rows - 1)):
+        for s in range(slices):
+            w0, w1 = s * o, min(s * o + o, out_chunks)
+            if w0 < w1:
+                want[t, w0:w1] = _wave_out(_fold_rows(table[id_], s * r, min(s * r + r, row_chunks)), w0, w1)
+    assert np.array_equal(got, want)

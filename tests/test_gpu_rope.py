@@ -286,3 +286,40 @@ def test_query_key_norm_rope_far_positions_and_weight_offsets(hip, dtype, far, o
         wq, wk = o.qk_norm_rope_bf16(qb, kb, *args)
         assert_bf16(wq, host_bits(rq), what="queries bf16")
         assert_bf16(wk, host_bits(rk), what="keys bf16")
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_query_key_norm_rope_with_weights_off_a_16_byte_boundary(hip, dtype):
+    # norm weights that start 4 bytes into a buffer (a slice): the fast body
+    # reads weights as 16-byte loads, so these take the general kernel
+    tokens, heads, kv, dim = 16, 32, 8, 128
+    rope = d.Rope(1e6, 128, d.RopeLayout.Neox)
+    q = gaussian(31, (tokens, heads, dim))
+    k = gaussian(32, (tokens, kv, dim))
+    qw = (1 + 0.1 * gaussian(33, dim)).astype(np.float32)
+    kw = (1 + 0.1 * gaussian(34, dim)).astype(np.float32)
+    p = np.arange(tokens, dtype=np.int32)
+    qw_at = dev_f32(np.concatenate([[7.0], qw]).astype(np.float32))[1:]
+    kw_at = dev_f32(np.concatenate([[7.0, 7.0, 7.0], kw]).astype(np.float32))[3:]
+    assert qw_at.data_ptr() % 16 == 4 and kw_at.data_ptr() % 16 == 12
+    args = (qw, kw, p, 1e-6, 0.0, rope.theta, rope.rotaryDimensions, int(rope.layout), rope.sections.code,
+            rope.sections.sizes)
+    norms = d.QueryKeyNorms(qw_at, kw_at, 1e-6, 0.0, rope)
+    step(f"queryKeyNormRope {dtype}, norm weights 4 and 12 bytes past a 16-byte boundary")
+    if dtype == "f32":
+        rq = torch.empty(q.shape, dtype=torch.float32, device=DEV)
+        rk = torch.empty(k.shape, dtype=torch.float32, device=DEV)
+        hip.queryKeyNormRope(dev_f32(q), dev_f32(k), norms, dev_i32(p), rq, rk)
+        torch.cuda.synchronize()
+        wq, wk = o.qk_norm_rope(q, k, *args)
+        assert_f32(wq, host_f32(rq), what="queries")
+        assert_f32(wk, host_f32(rk), what="keys")
+    else:
+        qb, kb = bf16_input(q), bf16_input(k)
+        rq = torch.empty(q.shape, dtype=torch.bfloat16, device=DEV)
+        rk = torch.empty(k.shape, dtype=torch.bfloat16, device=DEV)
+        hip.queryKeyNormRope(dev_bf16(qb), dev_bf16(kb), norms, dev_i32(p), rq, rk)
+        torch.cuda.synchronize()
+        wq, wk = o.qk_norm_rope_bf16(qb, kb, *args)
+        assert_bf16(wq, host_bits(rq), what="queries bf16")
+        assert_bf16(wk, host_bits(rk), what="keys bf16")

@@ -220,3 +220,79 @@ def test_every_downcall_passes_its_layout():
 @pytest.mark.parametrize("stem", ["drift_rms_norm", "drift_attention_inputs", "drift_qk_norm_rope"])
 def test_twins_take_the_same_arguments(stem):
     assert _lib.SIGNATURES[f"{stem}_f32"] == _lib.SIGNATURES[f"{stem}_bf16"]
+
+
+MILL = os.path.join(SCALA, "driftKernels.mill")
+MAKEFILE = os.path.join(ROOT, "drift_amd", "csrc", "Makefile")
+MODULE = os.path.join(SCALA, "drift", "runner", "native", "KernelModule.scala")
+BASE = os.path.join(SCALA, "drift", "runner", "ops", "DriftBase.scala")
+
+
+def make_variable(name):
+    """A Makefile variable's words (one assignment, continuation lines joined)."""
+    text = open(MAKEFILE).read().replace("\\\n", " ")
+    value = re.search(rf"^{name}\s*:?=\s*(.*)$", text, re.M).group(1)
+    return value.split()
+
+
+def test_the_build_task_puts_the_library_where_the_binding_loads_it():
+    # the task writes <dest>/lib/libdrift_kernels.so and serves <dest> as a
+    # resource root: the jar's resource /lib/libdrift_kernels.so, which
+    # DriftKernels.default() copies out and loads
+    mill = strip_comments(open(MILL).read())
+    assert re.search(r'val out = Task\.dest / "lib"', mill)
+    assert re.search(r'out / "libdrift_kernels\.so"', mill)
+    assert re.search(r"PathRef\(Task\.dest\)", mill)
+    assert re.search(r"super\.resources\(\) :\+ kernels\(\) :\+ driftKernels\(\)", mill)
+    binding = strip_comments(open(BINDING).read())
+    assert re.search(r'val Resource = "/lib/libdrift_kernels\.so"', binding)
+    assert "getResourceAsStream(Resource)" in binding
+    assert 'sys.props.get("drift.kernels")' in binding
+
+
+def test_the_build_task_compiles_what_the_makefile_compiles():
+    mill = strip_comments(open(MILL).read())
+    listed = re.search(r"driftSources = Seq\(([^)]*)\)", mill).group(1)
+    assert re.findall(r'"([^"]+)"', listed) == make_variable("SOURCES")
+    flags = re.findall(r'"([^"]+)"', re.search(r"driftFlags = Seq\(([^)]*)\)", mill).group(1))
+    make_flags = [f.replace("$(ARCH)", "gfx950") for f in make_variable("FLAGS")]
+    for flag in ("--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off"):
+        assert flag in flags and flag in make_flags, flag
+    # packed FP32 off in both: -Xclang -target-feature -Xclang -packed-fp32-ops
+    for words in (flags, make_flags):
+        i = words.index("-packed-fp32-ops")
+        assert words[i - 3:i] == ["-Xclang", "-target-feature", "-Xclang"]
+
+
+def test_kernel_modules_load_on_first_lookup():
+    # the runner's modules are made when the backend is built
+    # (ops/HipBase.scala:71-75,328-336) but hold no code for gfx950: the
+    # replacement KernelModule loads one only inside `module`, which only
+    # `function` reaches, and `close` unloads only a loaded one
+    text = strip_comments(open(MODULE).read())
+    assert re.search(r"final class KernelModule\(hip: HipRuntime, val name: String\) extends AutoCloseable", text)
+    body = text[text.index("private def module"):]
+    module_def = body[:body.index("def function")]
+    assert text.count("hip.loadModule(") == 1 and "hip.loadModule(" in module_def
+    assert re.search(r"def function\(functionName: String\): KernelFunction = hip\.function\(module, functionName\)",
+                     text)
+    close = text[text.index("def close()"):]
+    assert "handle.foreach(hip.unloadModule)" in close and "module" not in close.replace("unloadModule", "")
+    # nothing outside `module` touches the code object
+    outside = text.replace(module_def, "")
+    assert "loadModule(" not in outside.replace("unloadModule", "")
+
+
+def test_traced_downcalls_record_their_time():
+    # DRIFT_HIP_TRACE times every launch by name (native/HipRuntime.scala:318,
+    # 358-362); a downcall records under its entry point's name after the
+    # device has finished it
+    text = strip_comments(open(BASE).read())
+    downcall = text[text.index("protected def downcall"):]
+    downcall = downcall[:downcall.index("\n  }\n")]
+    assert "HipRuntime.Trace.on" in downcall
+    traced = downcall[downcall.index("HipRuntime.Trace.on"):downcall.index("} else")]
+    order = [traced.index(s) for s in ("System.nanoTime()", "drift.check(name, call)", "hip.synchronize()",
+                                       "HipRuntime.Trace.record(name, System.nanoTime() - from)")]
+    assert order == sorted(order)
+    assert "drift.check(name, call)" in downcall[downcall.index("} else"):]
