@@ -83,7 +83,7 @@ SIGNATURES = {
     "drift_wave_row_probe": (_I32, [_P, _I64, _I32, _P, _I64, _P, _I32, _I32, _P]),
 }
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 
 class NotBuilt(RuntimeError):

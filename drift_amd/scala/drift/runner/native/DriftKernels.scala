@@ -121,7 +121,7 @@ final class DriftKernels(path: Path) {
 object DriftKernels {
 
   /** `DRIFT_ABI_VERSION` of the header these bindings repeat. */
-  val AbiVersion = 8
+  val AbiVersion = 9
 
   /** Where the runner's build puts the library: the resource
     * `lib/libdrift_kernels.so` of the runner's jar (the `driftKernels` task

@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define DRIFT_ABI_VERSION 8
+#define DRIFT_ABI_VERSION 9
 
 /* Activation kinds: src/drift/runner/ops/Activation.scala:6-20. */
 enum {

@@ -23,7 +23,7 @@ def test_header_and_library_agree(lib):
 
 
 def test_version_and_error_text(lib):
-    assert lib.drift_abi_version() == _lib.ABI_VERSION == 8
+    assert lib.drift_abi_version() == _lib.ABI_VERSION == 9
     assert lib.drift_error_string(0).decode().lower().startswith("no error")
     assert lib.drift_error_string(1)
 
