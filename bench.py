@@ -29,11 +29,16 @@ cost of one call of each entry point (drift_amd/host/launch_cost).
 
 Printed: one JSON line. `value` is the step's algorithmic bytes (the reads
 and writes of the tensors each op names) over the step's wall time;
-`kernels` has each kernel's HIP-event time, GB/s, fraction of the 8 TB/s HBM
-peak, fraction of its ceiling and rows/s; `ceilings` is the streaming probe
-(drift_stream_mix) moving each long kernel's bytes in its read:write mix,
-for the gather also its own pattern with no decode (drift_row_probe: the
-rows its ids name read, its output written; `frac_of_row_probe`), the
+`kernels` has each kernel's HIP-event time (`us`: the median of five
+replays of its graph, the first of them the timed step's, `us_step`), GB/s,
+fraction of the 8 TB/s HBM peak, fraction of its ceiling and rows/s;
+`ceilings` holds, for each long kernel, the fastest probe moving its bytes
+in its read:write mix with nothing else (drift_stream_mix: blocks that only
+read or only write; drift_wave_copy: one-wave blocks each reading its share
+and then writing its share, the kernels' own shape and the tighter at the
+prefill sizes), for the gather also its own pattern with no decode
+(drift_row_probe and drift_wave_row_probe: the rows its ids name read, its
+output written, by a block or by 1 to 8 waves an id; `frac_of_row_probe`), the
 reference's streaming read (drift_read_sum_f32x4) over 1 GiB, and the
 per-launch floor of a graph replay (`launch_floor`: one block writing one
 16-byte chunk), which the decode shapes' few microseconds sit on. A probe's
@@ -74,6 +79,7 @@ from drift_amd import ops as d  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
 MATCHED_ROUNDS = 7  # alternations of each kernel with its probe
+GRAPH_ROUNDS = 5  # replays of each kernel's graph: the first is the timed step, `us` the median
 MALL_BYTES = 512 << 20
 DEV = "cuda:0"
 
@@ -92,7 +98,8 @@ class Kernel:
         self.launch = launch
         self.cpu = None  # (sample description, seconds for the sample, fraction of a call the sample is)
         self.cpu_all = None  # (threads, seconds for the same sample split across them)
-        self.graph_ms = None  # average launch, replayed from a captured graph
+        self.graph_ms = None  # average launch, replayed from a captured graph (median over the rounds)
+        self.step_ms = None  # the same in the timed step's replay
         self.matched_ms = None  # the same, in alternation with its probe (median replay)
         self.eager_ms = None  # average launch, each made from Python through ctypes
         self.ceiling = None  # the stream probe at this kernel's bytes and read/write mix
@@ -689,11 +696,15 @@ def read_probe(lib, gib_bytes: int, blocks: int, name: str) -> Kernel:
     return probe
 
 
-def time_graphs(kernels, steps: int, warmup: int) -> float:
+def time_graphs(kernels, steps: int, warmup: int, rounds: int = 1) -> float:
     """Each kernel's `steps` launches captured in a HIP graph (rotating its
     buffer sets), replayed with one event pair around the replay on the
     replaying stream: the average launch is the span over `steps`, with no
-    host call in it. Returns the wall time of all the replays."""
+    host call in it. The first round of replays (every kernel once, in
+    order) is the timed region: its wall time is returned and each kernel's
+    figure in it kept as `step_ms`. Further rounds, after it, replay the same
+    graphs in the same order; `graph_ms` is each kernel's median over all
+    rounds, so one slow replay does not stand for the kernel."""
     stream = torch.cuda.current_stream()
     here = ctypes.c_void_p(stream.cuda_stream)
     graphs = []
@@ -711,16 +722,23 @@ def time_graphs(kernels, steps: int, warmup: int) -> float:
     for g in graphs:
         g.replay()
     torch.cuda.synchronize()
-    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in kernels]
-    t0 = time.perf_counter()
-    for g, (start, end) in zip(graphs, events):
-        start.record(stream)
-        g.replay()
-        end.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    for k, (start, end) in zip(kernels, events):
-        k.graph_ms = start.elapsed_time(end) / steps
+    times = [[] for _ in kernels]
+    wall = None
+    for r in range(rounds):
+        events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in kernels]
+        t0 = time.perf_counter()
+        for g, (start, end) in zip(graphs, events):
+            start.record(stream)
+            g.replay()
+            end.record(stream)
+        torch.cuda.synchronize()
+        if r == 0:
+            wall = time.perf_counter() - t0
+        for j, (start, end) in enumerate(events):
+            times[j].append(start.elapsed_time(end) / steps)
+    for k, t in zip(kernels, times):
+        k.step_ms = t[0]
+        k.graph_ms = statistics.median(t)
     del graphs
     return wall
 
@@ -846,7 +864,7 @@ def main():
     # rise, and a 17 us kernel timed right after the decode kernels' short
     # launches ran 25% slower than the same kernel after a long one
     largest_first = sorted(kernels, key=lambda k: k.bytes, reverse=True)
-    wall = time_graphs(largest_first, args.steps, args.warmup)
+    wall = time_graphs(largest_first, args.steps, args.warmup, rounds=GRAPH_ROUNDS)
     time_eager(largest_first, args.steps)
     time_graphs([p for group in probes.values() for p in group] + [p for group in rows_probes.values() for p in group]
                 + reads + floors, args.steps, args.warmup)
@@ -931,7 +949,8 @@ def main():
         avg = k.graph_ms
         gbs = k.bytes / (avg * 1e-3) / 1e9
         table[k.name] = {
-            "config": k.config, "us": round(avg * 1e3, 2), "us_eager": round(k.eager_ms * 1e3, 2), "bytes": k.bytes,
+            "config": k.config, "us": round(avg * 1e3, 2), "us_step": round(k.step_ms * 1e3, 2),
+            "us_eager": round(k.eager_ms * 1e3, 2), "bytes": k.bytes,
             "GB_s": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
             "rows_per_s": round(k.rows / (avg * 1e-3), 1),
         }
@@ -940,8 +959,9 @@ def main():
             table[k.name]["frac_of_probe_matched"] = ceilings[k.name]["matched"]["frac_of_probe"]
             if "row_probe" in ceilings[k.name]:
                 table[k.name]["frac_of_row_probe"] = round(gbs / ceilings[k.name]["row_probe"]["GB_s"], 4)
+    # the roofline kernel's launches as the timed step replayed them
     dominant = max(kernels, key=lambda k: k.graph_ms)
-    dom_avg = dominant.graph_ms
+    dom_avg = dominant.step_ms
     achieved = dominant.bytes / (dom_avg * 1e-3) / 1e9
     # HBM bytes per launch are not measured in this run (counters need a
     # profiler pass of their own): they come from the committed counter

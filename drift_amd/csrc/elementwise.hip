@@ -272,17 +272,19 @@ int activation(const char* entry, const T* x, T* out, int64_t n, int32_t kind, f
   const hipStream_t s = (hipStream_t)stream;
   constexpr int N = Chunk<T>::N;
   if (aligned16(x) && aligned16(out)) {
-    const unsigned grid = grid_for(ceil_div(n, N), 256, kOneShotBlocks);
+    // one-wave blocks: GELU-tanh over [65520, 3072] bf16 in place 123.5 us
+    // in 256-thread blocks against 120.2
+    const unsigned grid = grid_for(ceil_div(n, N), kWave, kOneShotBlocks);
     switch (kind) {
       case DRIFT_SILU:
-        hipLaunchKernelGGL((activation_kernel<T, DRIFT_SILU>), dim3(grid), dim3(256), 0, s, x, out, n, kind, scale);
+        hipLaunchKernelGGL((activation_kernel<T, DRIFT_SILU>), dim3(grid), dim3(kWave), 0, s, x, out, n, kind, scale);
         break;
       case DRIFT_GELU_TANH:
-        hipLaunchKernelGGL((activation_kernel<T, DRIFT_GELU_TANH>), dim3(grid), dim3(256), 0, s, x, out, n, kind,
+        hipLaunchKernelGGL((activation_kernel<T, DRIFT_GELU_TANH>), dim3(grid), dim3(kWave), 0, s, x, out, n, kind,
                            scale);
         break;
       default:
-        hipLaunchKernelGGL((activation_kernel<T, -1>), dim3(grid), dim3(256), 0, s, x, out, n, kind, scale);
+        hipLaunchKernelGGL((activation_kernel<T, -1>), dim3(grid), dim3(kWave), 0, s, x, out, n, kind, scale);
         break;
     }
   } else {

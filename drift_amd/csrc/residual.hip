@@ -16,7 +16,7 @@
 //
 // Layout: x, y, out row-major [rows, cols] of T; a lane takes one 16-byte
 // chunk (4 F32 or 8 BF16) of the flat tensor and the grid covers it in one
-// pass. A chunk's row comes from a double multiply by
+// pass, in one-wave blocks or 256-thread blocks by the op. A chunk's row comes from a double multiply by
 // 1 / chunks-per-row, corrected by one step, rather than a 64-bit division.
 #include "common.hpp"
 
@@ -152,8 +152,13 @@ int row_map(const char* entry, const T* x, const T* y, const float* v, T* out, R
     m.row_chunks = m.cols / N;
     m.row_inverse = 1.0 / (double)m.row_chunks;
     const int64_t total = values / N;
-    hipLaunchKernelGGL((row_map_chunks<T, OP>), dim3(grid_for(total, 256, kOneShotBlocks)), dim3(256), 0, s, x, y,
-                       v, out, m, total);
+    // one-wave blocks where they stream faster (gatedAdd 192 -> 183 us,
+    // rowGatedAdd 185 -> 182 us at [65520, 3072] bf16); the ops reading two
+    // or one F32 table rows a value keep 256-thread blocks (modulateChunks
+    // 407 against 414 us in one-wave blocks, gatedAddChunk even)
+    constexpr int kBlock = OP == MODULATE_CHUNKS || OP == GATED_ADD_CHUNK ? 256 : 64;
+    hipLaunchKernelGGL((row_map_chunks<T, OP>), dim3(grid_for(total, kBlock, kOneShotBlocks)), dim3(kBlock), 0, s, x,
+                       y, v, out, m, total);
   } else {
     hipLaunchKernelGGL((row_map_values<T, OP>), dim3(grid_for(values, 256, 8192)), dim3(256), 0, s, x, y, v, out, m,
                        values, 1.0 / (double)m.cols);
