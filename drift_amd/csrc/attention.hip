@@ -53,8 +53,9 @@ struct Extras {
 // written and *bad_page is set.
 template <typename T>
 __device__ __forceinline__ bool cache_place(const Extras<T>& e, int64_t t, int kv_heads, int dim, int kv,
-                                            int64_t& key, int64_t& value, int64_t page) {
+                                            int64_t& key, int64_t& value) {
   const int64_t position = e.start + t;
+  const int64_t page = e.page_table[position / e.page_size];
   const int64_t offset = position % e.page_size;
   if (page < 0 || page >= e.pages) {
     if (e.bad_page) *e.bad_page = 1;
@@ -65,10 +66,17 @@ __device__ __forceinline__ bool cache_place(const Extras<T>& e, int64_t t, int k
   return true;
 }
 
+// The key row alone, the token's page and its place in the page already
+// known (as cache_place, without the division).
 template <typename T>
-__device__ __forceinline__ bool cache_place(const Extras<T>& e, int64_t t, int kv_heads, int dim, int kv,
-                                            int64_t& key, int64_t& value) {
-  return cache_place(e, t, kv_heads, dim, kv, key, value, e.page_table[(e.start + t) / e.page_size]);
+__device__ __forceinline__ bool key_place(const Extras<T>& e, int32_t page, uint32_t in_page, int kv_heads, int dim,
+                                          int kv, int64_t& key) {
+  if (page < 0 || page >= e.pages) {
+    if (e.bad_page) *e.bad_page = 1;
+    return false;
+  }
+  key = (((int64_t)page * e.page_size + in_page) * kv_heads + kv) * dim;
+  return true;
 }
 
 // F32 -> F16 bits, to nearest even (v_cvt_f16_f32): Float.floatToFloat16's
@@ -326,11 +334,19 @@ __device__ __forceinline__ void qk_wave_heads(const T* q, const T* k, T* q_out, 
   // for irregular sums: each of those cost about 1 us.
   constexpr int kPairsPerLane = (half + kWave - 1) / kWave;
   const int32_t position = positions[t];  // single-section rope: one position a token
-  // with the cache, the token's page (read with the small operands, not
-  // after the turn, where the keys' stores would wait for it)
-  int64_t page = 0;
+  // with the cache, a key wave's page and the token's place in it, divided
+  // and read with the small operands, not after the turn, where the keys'
+  // stores would wait for them (cache positions are below 2^32: start and
+  // the tokens are int32 and not negative, so the quotient is 32-bit)
+  int32_t page = 0;  // widened only where the keys' stores use it, so nothing waits for it before
+  uint32_t in_page = 0;
   if constexpr (EXTRAS) {
-    if (e.keys) page = e.page_table[(e.start + t) / e.page_size];
+    if (e.keys && (!FAST || !query)) {
+      const uint32_t cached = (uint32_t)e.start + (uint32_t)t;
+      const uint32_t slot = cached / (uint32_t)e.page_size;
+      in_page = cached - slot * (uint32_t)e.page_size;
+      page = e.page_table[slot];
+    }
   }
   float inverse[kPairsPerLane];
 #pragma unroll
@@ -439,8 +455,8 @@ __device__ __forceinline__ void qk_wave_heads(const T* q, const T* k, T* q_out, 
         *reinterpret_cast<uint4*>(gh + d0) = g0;
         *reinterpret_cast<uint4*>(gh + d1) = g1;
       }
-      int64_t key, value;
-      if (!query && e.keys && cache_place(e, t, a.kv_heads, dim, hh - a.q_heads, key, value, page)) {
+      int64_t key;
+      if (!query && e.keys && key_place(e, page, in_page, a.kv_heads, dim, hh - a.q_heads, key)) {
         store_f16<N>(e.keys + key + d0, v0);
         store_f16<N>(e.keys + key + d1, v1);
       }
