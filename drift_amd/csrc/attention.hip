@@ -334,20 +334,6 @@ __device__ __forceinline__ void qk_wave_heads(const T* q, const T* k, T* q_out, 
   // for irregular sums: each of those cost about 1 us.
   constexpr int kPairsPerLane = (half + kWave - 1) / kWave;
   const int32_t position = positions[t];  // single-section rope: one position a token
-  // with the cache, a key wave's page and the token's place in it, divided
-  // and read with the small operands, not after the turn, where the keys'
-  // stores would wait for them (cache positions are below 2^32: start and
-  // the tokens are int32 and not negative, so the quotient is 32-bit)
-  int32_t page = 0;  // widened only where the keys' stores use it, so nothing waits for it before
-  uint32_t in_page = 0;
-  if constexpr (EXTRAS) {
-    if (e.keys && (!FAST || !query)) {
-      const uint32_t cached = (uint32_t)e.start + (uint32_t)t;
-      const uint32_t slot = cached / (uint32_t)e.page_size;
-      in_page = cached - slot * (uint32_t)e.page_size;
-      page = e.page_table[slot];
-    }
-  }
   float inverse[kPairsPerLane];
 #pragma unroll
   for (int u = 0; u < kPairsPerLane; ++u) inverse[u] = p.inverse[min(lane + u * kWave, half - 1)];
@@ -379,6 +365,20 @@ __device__ __forceinline__ void qk_wave_heads(const T* q, const T* k, T* q_out, 
       const T* gh = q + (t * a.q_heads + min(hc, a.q_heads - 1)) * a.q_stride + dim;
       g0 = Chunk<T>::load_raw(gh + d0);
       g1 = Chunk<T>::load_raw(gh + d1);
+    }
+  }
+  // with the cache, a key wave's page and the token's place in it, divided
+  // and read once the heads' loads are issued and before the turn, where the
+  // keys' stores would wait for them (cache positions are below 2^32: start
+  // and the tokens are int32 and not negative, so the quotient is 32-bit)
+  int32_t page = 0;  // widened only where the keys' stores use it, so nothing waits for it before
+  uint32_t in_page = 0;
+  if constexpr (EXTRAS) {
+    if (e.keys && (!FAST || !query)) {
+      const uint32_t cached = (uint32_t)e.start + (uint32_t)t;
+      const uint32_t slot = cached / (uint32_t)e.page_size;
+      in_page = cached - slot * (uint32_t)e.page_size;
+      page = e.page_table[slot];
     }
   }
   // the token's cos and sin, a pair a lane, into the wave's LDS
