@@ -16,8 +16,10 @@
 //
 // Layout: x, y, out row-major [rows, cols] of T; a lane takes one 16-byte
 // chunk (4 F32 or 8 BF16) of the flat tensor and the grid covers it in one
-// pass, in one-wave blocks or 256-thread blocks by the op. A chunk's row comes from a double multiply by
-// 1 / chunks-per-row, corrected by one step, rather than a 64-bit division.
+// pass, in one-wave blocks or 256-thread blocks by the op. A chunk's row
+// comes from a double multiply by 1 / chunks-per-row, corrected by one step,
+// rather than a 64-bit division; gatedAdd takes its row and sample from the
+// grid where they fit it.
 #include "common.hpp"
 
 #include <initializer_list>
@@ -62,11 +64,16 @@ struct Operands {
 
   __device__ __forceinline__ void load(const T* xs, const T* ys, const float* v, const RowMap& m, int64_t i) {
     const int64_t r = quotient(i, m.row_chunks, m.row_inverse);
-    const int c = (int)(i - r * m.row_chunks) * N;
+    load_at(xs, ys, v, m, i, r, (int)(i - r * m.row_chunks) * N, OP == GATED_ADD ? quotient(r, m.per, m.per_inverse) : 0);
+  }
+
+  // chunk i, which is value c of row r (of sample `sample`, gatedAdd)
+  __device__ __forceinline__ void load_at(const T* xs, const T* ys, const float* v, const RowMap& m, int64_t i,
+                                          int64_t r, int c, int64_t sample) {
     x = Chunk<T>::load_raw(xs + i * N);
     if constexpr (OP != MODULATE_CHUNKS) y = Chunk<T>::load_raw(ys + i * N);
     if constexpr (OP == GATED_ADD) {
-      load_floats<N, false>(v + quotient(r, m.per, m.per_inverse) * m.cols + c, a);
+      load_floats<N, false>(v + sample * m.cols + c, a);
     } else if constexpr (OP == ROW_GATED_ADD) {
       const float g = v[r];
 #pragma unroll
@@ -110,6 +117,20 @@ __global__ void __launch_bounds__(256) row_map_chunks(const T* x, const T* y, co
 }
 
 // Any width and alignment: one value per thread.
+// The row from the grid: blockIdx.x a wave's chunks of the row, blockIdx.y
+// the row within sample blockIdx.z, so no lane divides. For rows of whole
+// waves' chunks and at most 65,535 rows a sample.
+template <typename T, int OP>
+__global__ void __launch_bounds__(64) row_map_by_row(const T* x, const T* y, const float* v, T* out, RowMap m) {
+  constexpr int N = Chunk<T>::N;
+  const int64_t r = (int64_t)blockIdx.z * gridDim.y + blockIdx.y;
+  const int c = (int)blockIdx.x * 64 + (int)threadIdx.x;
+  const int64_t i = r * m.row_chunks + c;
+  Operands<T, OP> p;
+  p.load_at(x, y, v, m, i, r, c * N, blockIdx.z);
+  p.apply(out, i);
+}
+
 template <typename T, int OP>
 __global__ void __launch_bounds__(256) row_map_values(const T* x, const T* y, const float* v, T* out, RowMap m,
                                                       int64_t total, double col_inverse) {
@@ -157,6 +178,17 @@ int row_map(const char* entry, const T* x, const T* y, const float* v, T* out, R
     // or one F32 table rows a value keep 256-thread blocks (modulateChunks
     // 407 against 414 us in one-wave blocks, gatedAddChunk even)
     constexpr int kBlock = OP == MODULATE_CHUNKS || OP == GATED_ADD_CHUNK ? 256 : 64;
+    // gatedAdd takes its row and sample from the grid where they fit it
+    // ([65520, 3072] bf16: 185.0-185.3 -> 179.9-182.3 us); the other ops
+    // measured even (gatedAddChunk) or slower (modulateChunks, 422 against
+    // 406 us) that way, and rowGatedAdd's rows do not fit
+    const int64_t samples = m.rows / m.per;
+    if (OP == GATED_ADD && m.row_chunks % 64 == 0 && m.row_chunks / 64 <= INT32_MAX && m.per <= 65535 &&
+        samples <= 65535 && samples * m.per == m.rows) {
+      hipLaunchKernelGGL((row_map_by_row<T, OP>), dim3((unsigned)(m.row_chunks / 64), (unsigned)m.per,
+                         (unsigned)samples), dim3(64), 0, s, x, y, v, out, m);
+      return launched(entry);
+    }
     hipLaunchKernelGGL((row_map_chunks<T, OP>), dim3(grid_for(total, kBlock, kOneShotBlocks)), dim3(kBlock), 0, s, x,
                        y, v, out, m, total);
   } else {
