@@ -16,7 +16,7 @@
 //
 // Layout: x, y, out row-major [rows, cols] of T; a lane takes one 16-byte
 // chunk (4 F32 or 8 BF16) of the flat tensor and the grid covers it in one
-// pass, in one-wave blocks or 256-thread blocks by the op. A chunk's row
+// pass, in one-wave blocks or 512-thread blocks by the op. A chunk's row
 // comes from a double multiply by 1 / chunks-per-row, corrected by one step,
 // rather than a 64-bit division; gatedAdd takes its row and sample from the
 // grid where they fit it.
@@ -106,7 +106,7 @@ struct Operands {
 };
 
 template <typename T, int OP>
-__global__ void __launch_bounds__(256) row_map_chunks(const T* x, const T* y, const float* v, T* out, RowMap m,
+__global__ void __launch_bounds__(512) row_map_chunks(const T* x, const T* y, const float* v, T* out, RowMap m,
                                                       int64_t total) {
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
@@ -175,9 +175,10 @@ int row_map(const char* entry, const T* x, const T* y, const float* v, T* out, R
     const int64_t total = values / N;
     // one-wave blocks where they stream faster (gatedAdd 192 -> 183 us,
     // rowGatedAdd 185 -> 182 us at [65520, 3072] bf16); the ops reading two
-    // or one F32 table rows a value keep 256-thread blocks (modulateChunks
-    // 407 against 414 us in one-wave blocks, gatedAddChunk even)
-    constexpr int kBlock = OP == MODULATE_CHUNKS || OP == GATED_ADD_CHUNK ? 256 : 64;
+    // or one F32 table rows a value take 512-thread blocks (modulateChunks
+    // 393 us against 406 in 256-thread blocks, 414 in one-wave blocks;
+    // gatedAddChunk 307 against 315)
+    constexpr int kBlock = OP == MODULATE_CHUNKS || OP == GATED_ADD_CHUNK ? 512 : 64;
     // gatedAdd takes its row and sample from the grid where they fit it
     // ([65520, 3072] bf16: 185.0-185.3 -> 179.9-182.3 us); the other ops
     // measured even (gatedAddChunk) or slower (modulateChunks, 422 against
