@@ -36,7 +36,8 @@ fraction of the 8 TB/s HBM peak, fraction of its ceiling and rows/s;
 in its read:write mix with nothing else (drift_stream_mix: blocks that only
 read or only write; drift_wave_copy: one-wave blocks each reading its share
 and then writing its share, the kernels' own shape and the tighter at the
-prefill sizes), for the gather also its own pattern with no decode
+prefill sizes; drift_block_copy: the same waves in 512-thread blocks, the
+shape of the ops that read F32 table rows), for the gather also its own pattern with no decode
 (drift_row_probe and drift_wave_row_probe: the rows its ids name read, its
 output written, by a block or by 1 to 8 waves an id; `frac_of_row_probe`), the
 reference's streaming read (drift_read_sum_f32x4) over 1 GiB, and the
@@ -615,18 +616,20 @@ def ceiling_probes(k: Kernel, lib) -> list:
     """The probes moving k's read and write bytes with nothing else, over
     buffer sets totalling more than 512 MB like the kernel's: the stream
     probe (drift_stream_mix: 256-thread blocks that only read or only write,
-    1, 2 or 4 chunks a lane) and the one-wave probe (drift_wave_copy: each
+    1, 2 or 4 chunks a lane), the one-wave probe (drift_wave_copy: each
     one-wave block reading its share and then writing its share, 1, 2, 4 or
-    8 chunks a lane, the shape the fused kernels take). The fastest is k's
-    ceiling."""
+    8 chunks a lane, the shape most fused kernels take) and the same waves in
+    512-thread blocks (drift_block_copy, 1, 2 or 4 chunks a lane). The
+    fastest is k's ceiling."""
     reads = -(-k.read_bytes // 16)
     writes = -(-(k.bytes - k.read_bytes) // 16)
     n = sets_for(16 * (reads + writes))
     buffers = [(torch.empty(max(reads, 1) * 16, dtype=torch.uint8, device=DEV).fill_(7),
                 torch.empty(writes * 16, dtype=torch.uint8, device=DEV)) for _ in range(n)]
     probes = []
-    for entry, shape, lanes in (("drift_stream_mix", "stream_mix", (1, 2, 4)),
-                                ("drift_wave_copy", "wave_copy", (1, 2, 4, 8))):
+    for entry, shape, lanes, extra in (("drift_stream_mix", "stream_mix", (1, 2, 4), ()),
+                                       ("drift_wave_copy", "wave_copy", (1, 2, 4, 8), ()),
+                                       ("drift_block_copy", "block_copy_8_waves", (1, 2, 4), (8,))):
         for per in lanes:
             probe = Kernel(f"ceiling of {k.name}", f"{shape}: {reads} chunks read, {writes} written, {per} a lane",
                            16 * (reads + writes), k.rows, None, n, read_bytes=16 * reads)
@@ -636,7 +639,7 @@ def ceiling_probes(k: Kernel, lib) -> list:
             for src, dst in buffers:
                 probe.calls.append((entry, getattr(lib, entry),
                                     (ctypes.c_void_p(src.data_ptr()), reads, ctypes.c_void_p(dst.data_ptr()), writes,
-                                     per)))
+                                     per) + extra))
             probes.append(probe)
     return probes
 

@@ -80,10 +80,11 @@ SIGNATURES = {
     "drift_stream_mix": (_I32, [_P, _I64, _P, _I64, _I32, _P]),
     "drift_row_probe": (_I32, [_P, _I64, _I32, _P, _I64, _P, _I32, _P]),
     "drift_wave_copy": (_I32, [_P, _I64, _P, _I64, _I32, _P]),
+    "drift_block_copy": (_I32, [_P, _I64, _P, _I64, _I32, _I32, _P]),
     "drift_wave_row_probe": (_I32, [_P, _I64, _I32, _P, _I64, _P, _I32, _I32, _P]),
 }
 
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 
 class NotBuilt(RuntimeError):

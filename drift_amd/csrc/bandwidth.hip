@@ -126,7 +126,7 @@ __global__ void __launch_bounds__(256) row_probe_kernel(const uint4* table, int6
 template <int R, int W>
 __device__ __forceinline__ void wave_part(const uint4* src, int64_t r0, int64_t r1, uint4* dst, int64_t w0,
                                           int64_t w1) {
-  const int lane = threadIdx.x;
+  const int lane = threadIdx.x % kWave;
   uint4 v[R];
 #pragma unroll
   for (int k = 0; k < R; ++k) {
@@ -153,6 +153,16 @@ __global__ void __launch_bounds__(kWave) wave_copy_kernel(const uint4* src, int6
                                                           int64_t write_chunks, int rpw, int wpw) {
   const int64_t b = blockIdx.x;
   wave_part<R, W>(src, b * rpw, min(b * rpw + rpw, read_chunks), dst, b * wpw, min(b * wpw + wpw, write_chunks));
+}
+
+// the same in blocks of several waves: wave w of block k is wave b = k
+// waves_per_block + w (a wave past the last finds both its ranges empty)
+template <int R, int W>
+__global__ void __launch_bounds__(1024) block_copy_kernel(const uint4* src, int64_t read_chunks, uint4* dst,
+                                                          int64_t write_chunks, int rpw, int wpw) {
+  const int64_t b = (int64_t)blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
+  wave_part<R, W>(src, min(b * rpw, read_chunks), min(b * rpw + rpw, read_chunks), dst, min(b * wpw, write_chunks),
+                  min(b * wpw + wpw, write_chunks));
 }
 
 // wave b takes slice s = b % slices of id t = b / slices (clamped into the
@@ -202,6 +212,15 @@ struct WaveCopyLaunch {
                  int wpw) {
     hipLaunchKernelGGL((wave_copy_kernel<R, W>), dim3((unsigned)waves), dim3(kWave), 0, s, in, reads, out, writes,
                        rpw, wpw);
+  }
+};
+
+template <int R, int W>
+struct BlockCopyLaunch {
+  static void go(int64_t blocks, int waves_per_block, hipStream_t s, const uint4* in, int64_t reads, uint4* out,
+                 int64_t writes, int rpw, int wpw) {
+    hipLaunchKernelGGL((block_copy_kernel<R, W>), dim3((unsigned)blocks), dim3(kWave * waves_per_block), 0, s, in,
+                       reads, out, writes, rpw, wpw);
   }
 };
 
@@ -281,13 +300,18 @@ extern "C" int drift_row_probe(const void* table, int64_t rows, int32_t row_chun
   return launched(entry);
 }
 
-extern "C" int drift_wave_copy(const void* src, int64_t read_chunks, void* dst, int64_t write_chunks,
-                               int32_t per_lane, void* stream) {
-  const char* entry = "drift_wave_copy";
+namespace drift {
+namespace {
+
+// drift_wave_copy in blocks of waves_per_block waves (1: one-wave blocks)
+int copy_probe(const char* entry, const void* src, int64_t read_chunks, void* dst, int64_t write_chunks,
+               int32_t per_lane, int32_t waves_per_block, void* stream) {
   clear_error();
   if (read_chunks < 0 || write_chunks < 1 || lanes_cover((int64_t)per_lane * kWave) != per_lane)
     return refuse("%s: %lld chunks read, %lld written, %d a lane (at least one written; 1, 2, 4 or 8 a lane)", entry,
                   (long long)read_chunks, (long long)write_chunks, per_lane);
+  if (waves_per_block < 1 || waves_per_block > 16 || (waves_per_block & (waves_per_block - 1)) != 0)
+    return refuse("%s: %d waves a block (1, 2, 4, 8 or 16)", entry, waves_per_block);
   if ((read_chunks > 0 && !src) || !dst) return refuse("%s: null src or dst", entry);
   if ((read_chunks > 0 && !aligned16(src)) || !aligned16(dst)) return refuse("%s: src or dst is not 16-byte aligned", entry);
   const int64_t waves = std::max(ceil_div(read_chunks, (int64_t)per_lane * kWave),
@@ -296,9 +320,27 @@ extern "C" int drift_wave_copy(const void* src, int64_t read_chunks, void* dst, 
   // a wave's share, ceil(chunks / waves), is at most per_lane * 64
   const int64_t rpw = ceil_div(read_chunks, waves), wpw = ceil_div(write_chunks, waves);
   const int r = std::max(lanes_cover(rpw), 1), w = lanes_cover(wpw);
-  launch_rw<WaveCopyLaunch>(r, w, waves, (hipStream_t)stream, static_cast<const uint4*>(src), read_chunks,
-                            static_cast<uint4*>(dst), write_chunks, (int)rpw, (int)wpw);
+  if (waves_per_block == 1)
+    launch_rw<WaveCopyLaunch>(r, w, waves, (hipStream_t)stream, static_cast<const uint4*>(src), read_chunks,
+                              static_cast<uint4*>(dst), write_chunks, (int)rpw, (int)wpw);
+  else
+    launch_rw<BlockCopyLaunch>(r, w, ceil_div(waves, (int64_t)waves_per_block), (int)waves_per_block,
+                               (hipStream_t)stream, static_cast<const uint4*>(src), read_chunks,
+                               static_cast<uint4*>(dst), write_chunks, (int)rpw, (int)wpw);
   return launched(entry);
+}
+
+}  // namespace
+}  // namespace drift
+
+extern "C" int drift_wave_copy(const void* src, int64_t read_chunks, void* dst, int64_t write_chunks,
+                               int32_t per_lane, void* stream) {
+  return copy_probe("drift_wave_copy", src, read_chunks, dst, write_chunks, per_lane, 1, stream);
+}
+
+extern "C" int drift_block_copy(const void* src, int64_t read_chunks, void* dst, int64_t write_chunks,
+                                int32_t per_lane, int32_t waves_per_block, void* stream) {
+  return copy_probe("drift_block_copy", src, read_chunks, dst, write_chunks, per_lane, waves_per_block, stream);
 }
 
 extern "C" int drift_wave_row_probe(const void* table, int64_t rows, int32_t row_chunks, const int32_t* ids,

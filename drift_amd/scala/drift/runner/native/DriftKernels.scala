@@ -102,6 +102,7 @@ final class DriftKernels(path: Path) {
   val streamMix = bind("drift_stream_mix", P, JAVA_LONG, P, JAVA_LONG, JAVA_INT, P)
   val rowProbe = bind("drift_row_probe", P, JAVA_LONG, JAVA_INT, P, JAVA_LONG, P, JAVA_INT, P)
   val waveCopy = bind("drift_wave_copy", P, JAVA_LONG, P, JAVA_LONG, JAVA_INT, P)
+  val blockCopy = bind("drift_block_copy", P, JAVA_LONG, P, JAVA_LONG, JAVA_INT, JAVA_INT, P)
   val waveRowProbe = bind("drift_wave_row_probe", P, JAVA_LONG, JAVA_INT, P, JAVA_LONG, P, JAVA_INT, JAVA_INT, P)
 
   /** A downcall's result: a nonzero code becomes a HipException carrying the
@@ -121,7 +122,7 @@ final class DriftKernels(path: Path) {
 object DriftKernels {
 
   /** `DRIFT_ABI_VERSION` of the header these bindings repeat. */
-  val AbiVersion = 9
+  val AbiVersion = 10
 
   /** Where the runner's build puts the library: the resource
     * `lib/libdrift_kernels.so` of the runner's jar (the `driftKernels` task

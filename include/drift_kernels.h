@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define DRIFT_ABI_VERSION 9
+#define DRIFT_ABI_VERSION 10
 
 /* Activation kinds: src/drift/runner/ops/Activation.scala:6-20. */
 enum {
@@ -456,6 +456,10 @@ int drift_row_probe(const void* table, int64_t rows, int32_t row_chunks, const i
  * written). Each lane's written chunks hold the XOR of the chunks it read,
  * the first word also XORed with the chunk's place in the wave's share; src
  * and dst 16-byte aligned. No counterpart in the reference.
+ * drift_block_copy: the same waves in blocks of waves_per_block waves (1, 2,
+ * 4, 8 or 16; 1 is drift_wave_copy), wave w of block k being wave
+ * k waves_per_block + w: the shape of the kernels that take several waves a
+ * block. No counterpart in the reference.
  * drift_wave_row_probe: a gather's bytes in the gather's own shape: `slices`
  * one-wave blocks per id, wave s of id t reading chunks [s r, (s + 1) r) of
  * table row ids[t] (clamped into the table; r = row_chunks / slices rounded
@@ -465,6 +469,8 @@ int drift_row_probe(const void* table, int64_t rows, int32_t row_chunks, const i
  * reference. */
 int drift_wave_copy(const void* src, int64_t read_chunks, void* dst, int64_t write_chunks, int32_t per_lane,
                     void* stream);
+int drift_block_copy(const void* src, int64_t read_chunks, void* dst, int64_t write_chunks, int32_t per_lane,
+                     int32_t waves_per_block, void* stream);
 int drift_wave_row_probe(const void* table, int64_t rows, int32_t row_chunks, const int32_t* ids, int64_t count,
                          void* out, int32_t out_chunks, int32_t slices, void* stream);
 

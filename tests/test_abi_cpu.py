@@ -23,7 +23,7 @@ def test_header_and_library_agree(lib):
 
 
 def test_version_and_error_text(lib):
-    assert lib.drift_abi_version() == _lib.ABI_VERSION == 9
+    assert lib.drift_abi_version() == _lib.ABI_VERSION == 10
     assert lib.drift_error_string(0).decode().lower().startswith("no error")
     assert lib.drift_error_string(1)
 
@@ -174,6 +174,10 @@ def test_wave_probes_refuse_bad_geometry(lib):
     assert "16 a lane" in refused(lib, "drift_wave_copy", p, 10, p, 10, 16, NULL)
     assert "null" in refused(lib, "drift_wave_copy", NULL, 10, p, 10, 1, NULL)
     assert "not 16-byte aligned" in refused(lib, "drift_wave_copy", p, 10, ctypes.c_void_p(8), 10, 1, NULL)
+    assert "3 waves a block" in refused(lib, "drift_block_copy", p, 10, p, 10, 1, 3, NULL)
+    assert "32 waves a block" in refused(lib, "drift_block_copy", p, 10, p, 10, 1, 32, NULL)
+    assert "0 waves a block" in refused(lib, "drift_block_copy", p, 10, p, 10, 1, 0, NULL)
+    assert "at least one written" in refused(lib, "drift_block_copy", p, 10, p, 0, 1, 8, NULL)
     assert "at most 512 chunks" in refused(lib, "drift_wave_row_probe", p, 10, 1025, p, 4, p, 8, 2, NULL)
     assert "at most 512 chunks" in refused(lib, "drift_wave_row_probe", p, 10, 16, p, 4, p, 600, 1, NULL)
     assert "0 waves a row" in refused(lib, "drift_wave_row_probe", p, 10, 16, p, 4, p, 8, 0, NULL)

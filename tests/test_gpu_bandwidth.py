@@ -93,18 +93,25 @@ def _wave_out(folded: np.ndarray, w0: int, w1: int) -> np.ndarray:
     return out
 
 
-@pytest.mark.parametrize("reads,writes,per", [(1, 1, 1), (1000, 3000, 2), (35651, 67108, 8), (0, 513, 1),
-                                              (2, 7000, 2), (9000, 5, 4), (4096, 4096, 4)])
-def test_wave_copy_folds_each_waves_reads_into_its_writes(reads, writes, per):
+@pytest.mark.parametrize("reads,writes,per,block", [(1, 1, 1, 1), (1000, 3000, 2, 1), (35651, 67108, 8, 1),
+                                                    (0, 513, 1, 1), (2, 7000, 2, 1), (9000, 5, 4, 1), (4096, 4096, 4, 1),
+                                                    (1000, 3000, 2, 8), (35651, 67108, 1, 16), (9000, 5, 4, 2),
+                                                    (4096, 4096, 4, 4), (1, 1, 1, 8)])
+def test_wave_copy_folds_each_waves_reads_into_its_writes(reads, writes, per, block):
     # wave b reads [b r, (b + 1) r) and writes [b w, (b + 1) w), r and w the
-    # even shares over max(reads, writes) / (64 per) waves, rounded up
-    step(f"wave_copy {reads} chunks read, {writes} written, {per} a lane")
+    # even shares over max(reads, writes) / (64 per) waves, rounded up, in
+    # blocks of `block` waves (drift_block_copy; 1: drift_wave_copy)
+    step(f"wave_copy {reads} chunks read, {writes} written, {per} a lane, {block} waves a block")
     rng = np.random.default_rng(reads + 7 * writes)
     chunks = rng.integers(0, 2**32, (max(reads, 1), 4), dtype=np.uint64).astype(np.uint32)
     src = torch.from_numpy(chunks.view(np.int32)).to(DEV)
     dst = torch.zeros((writes, 4), dtype=torch.int32, device=DEV)
-    _lib.call("drift_wave_copy", ctypes.c_void_p(src.data_ptr()), reads, ctypes.c_void_p(dst.data_ptr()), writes,
-              per, None)
+    if block == 1:
+        _lib.call("drift_wave_copy", ctypes.c_void_p(src.data_ptr()), reads, ctypes.c_void_p(dst.data_ptr()), writes,
+                  per, None)
+    else:
+        _lib.call("drift_block_copy", ctypes.c_void_p(src.data_ptr()), reads, ctypes.c_void_p(dst.data_ptr()),
+                  writes, per, block, None)
     got = dst.cpu().numpy().view(np.uint32)
     waves = max(-(-reads // (64 * per)), -(-writes // (64 * per)))
     r, w = -(-reads // waves), -(-writes // waves)
