@@ -477,7 +477,7 @@ template <typename T, int G, bool NEOX, bool EXTRAS, bool GATE, bool FAST, int P
 __global__ void __launch_bounds__(kWave) qk_norm_rope_wave(const T* q, const T* k, T* q_out, T* k_out,
                                                           const float* q_weight, const float* k_weight,
                                                           const int32_t* positions, QkArgs a, Extras<T> e,
-                                                          int waves_per_token) {
+                                                          int waves_per_token, int query_waves, bool keys_first) {
   constexpr int N = Chunk<T>::N;
   constexpr int dim = 2 * N * G;
   const RopeArgs& p = a.rope;
@@ -497,10 +497,28 @@ __global__ void __launch_bounds__(kWave) qk_norm_rope_wave(const T* q, const T* 
     }
     item -= e.tiles;
   }
-  // blocks number fewer than 2^31 (the launcher checks): 32-bit division
-  const uint32_t token = (uint32_t)item / (uint32_t)waves_per_token;
+  // the grid's waves in two runs, the heavier first, so that the launch ends
+  // on its shortest waves: every token's query waves (its first query_waves
+  // groups), then its key waves, or with keys_first the other way round.
+  // Without the cache C3's key wave takes 8 heads and a query wave 16, so the
+  // keys go last (QK 16.05-16.15 -> 15.72-15.80 us; keys first 16.48-16.54);
+  // with it a key wave also places and writes the cache, and goes first
+  // (19.45-19.61 against 19.78-19.90 token by token). Blocks number fewer
+  // than 2^31 (the launcher checks): 32-bit division.
+  const uint32_t tokens = (uint32_t)p.tokens, qw = (uint32_t)query_waves;
+  const uint32_t kw = (uint32_t)waves_per_token - qw;  // 0: token by token (qw is every wave)
+  const uint32_t first_run = tokens * (keys_first ? kw : qw), first_waves = keys_first ? kw : qw;
+  uint32_t token, group_u;
+  if ((uint32_t)item < first_run) {
+    token = (uint32_t)item / first_waves;
+    group_u = (uint32_t)item - token * first_waves + (keys_first ? qw : 0);
+  } else {
+    const uint32_t rest = (uint32_t)item - first_run, waves = keys_first ? qw : kw;
+    token = rest / waves;
+    group_u = rest - token * waves + (keys_first ? 0 : qw);
+  }
   const int64_t t = token;
-  const int group = (int)((uint32_t)item - token * (uint32_t)waves_per_token);
+  const int group = (int)group_u;
   qk_wave_heads<T, G, NEOX, EXTRAS, GATE, FAST, P>(q, k, q_out, k_out, q_weight, k_weight, positions, a, e, t, group,
                                                 reinterpret_cast<double2*>(lds));
 }
@@ -604,6 +622,11 @@ int qk_launch(const char* entry, const T* q, const T* k, T* q_out, T* k_out, con
   const bool fast = a.q_heads % heads_per_wave == 0 && a.offset == 0.0f;
   const int passes = fast && !EXTRAS && a.q_heads % (2 * heads_per_wave) == 0 ? 2 : 1;
   const int waves_per_token = (int)ceil_div(a.q_heads + a.kv_heads, heads_per_wave * passes);
+  // with the fast body a wave's heads are all queries or all keys, and the
+  // grid runs the query waves and the key waves apart (the key waves first
+  // when they write the cache, last otherwise); else token by token
+  const int query_waves = fast && a.kv_heads > 0 ? a.q_heads / (heads_per_wave * passes) : waves_per_token;
+  const bool keys_first = EXTRAS && e.keys != nullptr;
   Extras<T> ex = e;
   const int tile_heads = kTileHeads(dim);
   ex.tiles = EXTRAS && e.keys ? ((int64_t)(e.start + p.tokens - 1) / 16 - e.start / 16 + 1) *
@@ -616,13 +639,13 @@ int qk_launch(const char* entry, const T* q, const T* k, T* q_out, T* k_out, con
 #define DRIFT_QK_LAUNCH(G, NEOX, GATE)                                                                               \
   if (passes == 2)                                                                                                   \
     hipLaunchKernelGGL((qk_norm_rope_wave<T, G, NEOX, EXTRAS, GATE, true, EXTRAS ? 1 : 2>), grid, block, 0, st, q,  \
-                       k, q_out, k_out, q_weight, k_weight, positions, a, ex, waves_per_token);                      \
+                       k, q_out, k_out, q_weight, k_weight, positions, a, ex, waves_per_token, query_waves, keys_first);\
   else if (fast)                                                                                                     \
     hipLaunchKernelGGL((qk_norm_rope_wave<T, G, NEOX, EXTRAS, GATE, true, 1>), grid, block, 0, st, q, k, q_out,     \
-                       k_out, q_weight, k_weight, positions, a, ex, waves_per_token);                                \
+                       k_out, q_weight, k_weight, positions, a, ex, waves_per_token, query_waves, keys_first);      \
   else                                                                                                               \
     hipLaunchKernelGGL((qk_norm_rope_wave<T, G, NEOX, EXTRAS, GATE, false, 1>), grid, block, 0, st, q, k, q_out,    \
-                       k_out, q_weight, k_weight, positions, a, ex, waves_per_token)
+                       k_out, q_weight, k_weight, positions, a, ex, waves_per_token, query_waves, keys_first)
 #define DRIFT_QK_CASE(G)                                                                                             \
   case G:                                                                                                            \
     if (EXTRAS && e.gate) {                                                                                          \
