@@ -178,15 +178,16 @@ QK_CASES = [
     # two groups of heads a wave, the key waves' second group part-filled or empty
     (19, 16, 12, 128, d.Rope(1e6, 128, d.RopeLayout.Neox)),
     (11, 32, 4, 64, d.Rope(1e4, 64, d.RopeLayout.Interleaved)),
-    # keys one group a token: two tokens' keys a wave, the last wave one
-    # token when the count is odd; query waves a token 2 (a shift), 1 and 3
-    # (a division); bf16 heads of 128 and 64, F32 heads of 128
+    # the grid's query waves first and its key waves after them: odd token
+    # counts, one token, 1, 2 or 3 query waves a token; bf16 heads of 128 and
+    # 64, F32 heads of 128; no query heads at all
     (7, 32, 8, 128, d.Rope(1e6, 128, d.RopeLayout.Neox)),
     (1, 32, 8, 128, d.Rope(1e6, 128, d.RopeLayout.Neox)),
     (9, 16, 8, 128, d.Rope(1e6, 128, d.RopeLayout.Neox)),
     (5, 48, 8, 128, d.Rope(1e4, 128, d.RopeLayout.Interleaved)),
     (13, 8, 4, 128, d.Rope(1e6, 128, d.RopeLayout.Neox)),
     (6, 64, 16, 64, d.Rope(1e4, 64, d.RopeLayout.Interleaved)),
+    (5, 0, 8, 128, d.Rope(1e6, 128, d.RopeLayout.Neox)),
 ]
 
 
