@@ -167,3 +167,7 @@ def test_a_large_weight(hip):
     hip.embedding(table8, dev_i32(ids), out8)
     rows = o.to_bf16(r8.rows_of())
     assert_bits(rows[ids], host_bits(out8), "8192 ids")
+    step("rotated dequantize int8 [1000, 4096]")
+    whole = torch.empty((1000, 4096), dtype=torch.bfloat16, device=DEV)
+    hip.dequantize(table8, whole)
+    assert_bits(rows, host_bits(whole), "int8 [1000, 4096]")
