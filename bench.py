@@ -29,9 +29,14 @@ cost of one call of each entry point (drift_amd/host/launch_cost).
 
 Printed: one JSON line. `value` is the step's algorithmic bytes (the reads
 and writes of the tensors each op names) over the step's wall time;
-`kernels` has each kernel's HIP-event time (`us`: the median of five
-replays of its graph, the first of them the timed step's, `us_step`), GB/s,
-fraction of the 8 TB/s HBM peak, fraction of its ceiling and rows/s;
+`kernels` has each kernel's HIP-event times: `us`, its launch inside a
+graph, the slope between a replay of its K-launch graph and one of 4 K
+launches right after it (median of five such pairs), which leaves out the
+fixed start every replay pays before its first launch (about 18 us on
+MI355X, the same for every graph, so 0.9 us a launch at K = 20); `us_step`,
+its K-launch replay's span over K in the timed step, that start included;
+`us_replay`, the same over five replays. Then GB/s (from `us`), fraction of
+the 8 TB/s HBM peak, fraction of its ceiling and rows/s;
 `ceilings` holds, for each long kernel, the fastest probe moving its bytes
 in its read:write mix with nothing else (drift_stream_mix: blocks that only
 read or only write; drift_wave_copy: one-wave blocks each reading its share
@@ -45,8 +50,9 @@ per-launch floor of a graph replay (`launch_floor`: one block writing one
 16-byte chunk), which the decode shapes' few microseconds sit on. A probe's
 launches fall into two or three durations by clock and memory state, so
 each kernel is also replayed in alternation with its best probe
-(`ceilings[k]["matched"]`, and `frac_of_probe_matched`: the median replays'
-ratio under the same conditions);
+(`ceilings[k]["matched"]`, and `frac_of_probe_matched`: the ratio of their
+median launch slopes under the same conditions); every probe's `us` is its
+launch slope too;
 `roofline` is the dominant kernel's; `cpu_baseline` is the CPU reference
 arithmetic (the oracle) timed on a bounded sample of the same work on this
 host's cores, scaled to the whole step. With `--formats`, `formats` holds
@@ -80,7 +86,9 @@ from drift_amd import ops as d  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
 MATCHED_ROUNDS = 7  # alternations of each kernel with its probe
-GRAPH_ROUNDS = 5  # replays of each kernel's graph: the first is the timed step, `us` the median
+GRAPH_ROUNDS = 5  # replays of each kernel's graph: the first is the timed step
+LONG = 4  # the long graph beside each K-launch graph holds LONG x K launches
+SLOPES = True  # False (--no-slopes): no long graphs; `us` is then the K-launch replay's span over K
 MALL_BYTES = 512 << 20
 DEV = "cuda:0"
 
@@ -99,9 +107,11 @@ class Kernel:
         self.launch = launch
         self.cpu = None  # (sample description, seconds for the sample, fraction of a call the sample is)
         self.cpu_all = None  # (threads, seconds for the same sample split across them)
-        self.graph_ms = None  # average launch, replayed from a captured graph (median over the rounds)
+        self.launch_ms = None  # a launch inside a graph: the slope between K- and LONG x K-launch replays (median)
+        self.graph_ms = None  # a K-launch replay's span over K, its fixed start included (median over the rounds)
         self.step_ms = None  # the same in the timed step's replay
-        self.matched_ms = None  # the same, in alternation with its probe (median replay)
+        self.matched_ms = None  # the slope, in alternation with its probe (median round)
+        self.matched_replay_ms = None  # the K-launch replay's span over K in the same rounds (median)
         self.eager_ms = None  # average launch, each made from Python through ctypes
         self.ceiling = None  # the stream probe at this kernel's bytes and read/write mix
 
@@ -411,12 +421,13 @@ def time_formats(hip: d.HipOps, lib, steps: int, warmup: int) -> dict:
     time_graphs(kernels, steps, warmup)
     time_graphs([p for group in probes.values() for p in group], steps, warmup)
     for k in kernels:
-        k.ceiling = min(probes[k.name], key=lambda p: p.graph_ms)
+        k.ceiling = min(probes[k.name], key=lambda p: p.launch_ms)
     time_matched([[k, k.ceiling] for k in kernels], steps, MATCHED_ROUNDS)
     out = {}
     for k in kernels:
-        gbs = k.bytes / (k.graph_ms * 1e-3) / 1e9
-        out[k.name] = {"config": k.config, "us": round(k.graph_ms * 1e3, 2), "bytes": k.bytes, "GB_s": round(gbs, 1),
+        gbs = k.bytes / (k.launch_ms * 1e-3) / 1e9
+        out[k.name] = {"config": k.config, "us": round(k.launch_ms * 1e3, 2),
+                       "us_replay": round(k.graph_ms * 1e3, 2), "bytes": k.bytes, "GB_s": round(gbs, 1),
                        "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "probe_us": round(k.ceiling.matched_ms * 1e3, 2),
                        "frac_of_probe_matched": round(k.ceiling.matched_ms / k.matched_ms, 4)}
     for k in kernels:
@@ -699,28 +710,70 @@ def read_probe(lib, gib_bytes: int, blocks: int, name: str) -> Kernel:
     return probe
 
 
+def capture(k: Kernel, first: int, launches: int):
+    """A HIP graph of k's launches over buffer sets first, first + 1, ..."""
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        captured = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        for i in range(launches):
+            k.fire(first + i, captured)
+    return g
+
+
+def slopes(pairs, steps: int, rounds: int, stream):
+    """For each (K-launch graph, LONG x K-launch graph), `rounds` times in
+    turn: the two replayed back to back, an event before, between and after.
+    Returns, per pair, each round's K-launch span over K and its launch
+    slope, (long span - K span) / ((LONG - 1) K): a replay's fixed start
+    (the span from the event before it to its first launch, the same for
+    every graph, about 18 us here) cancels, and the slope is the launch's
+    own time inside a graph, the figure a kernel trace's average duration
+    gives."""
+    spans = [[] for _ in pairs]
+    slope = [[] for _ in pairs]
+    for g, long in pairs:  # a first replay of each, untimed
+        g.replay()
+        if long is not None:
+            long.replay()
+    torch.cuda.synchronize()
+    for _ in range(rounds):
+        events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in pairs]
+        for (g, long), (a, b, c) in zip(pairs, events):
+            a.record(stream)
+            g.replay()
+            b.record(stream)
+            if long is not None:
+                long.replay()
+            c.record(stream)
+        torch.cuda.synchronize()
+        for j, ((_, long), (a, b, c)) in enumerate(zip(pairs, events)):
+            short_ms = a.elapsed_time(b)
+            spans[j].append(short_ms / steps)
+            if long is not None:
+                slope[j].append((b.elapsed_time(c) - short_ms) / ((LONG - 1) * steps))
+    return spans, slope
+
+
 def time_graphs(kernels, steps: int, warmup: int, rounds: int = 1) -> float:
     """Each kernel's `steps` launches captured in a HIP graph (rotating its
     buffer sets), replayed with one event pair around the replay on the
-    replaying stream: the average launch is the span over `steps`, with no
-    host call in it. The first round of replays (every kernel once, in
+    replaying stream. The first round of replays (every kernel once, in
     order) is the timed region: its wall time is returned and each kernel's
-    figure in it kept as `step_ms`. Further rounds, after it, replay the same
-    graphs in the same order; `graph_ms` is each kernel's median over all
-    rounds, so one slow replay does not stand for the kernel."""
+    span over `steps` in it kept as `step_ms`. Further rounds, after it,
+    replay the same graphs in the same order; `graph_ms` is each kernel's
+    median span over `steps` over all rounds. Then `launch_ms`: the median
+    launch slope of each kernel's graph and a graph of LONG x `steps` of its
+    launches, replayed back to back (`slopes`), which leaves out the fixed
+    start that every replay's span carries."""
     stream = torch.cuda.current_stream()
     here = ctypes.c_void_p(stream.cuda_stream)
-    graphs = []
+    graphs, longs = [], []
     for k in kernels:
         for i in range(warmup):
             k.fire(i, here)
         torch.cuda.synchronize()
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            captured = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-            for i in range(steps):
-                k.fire(warmup + i, captured)
-        graphs.append(g)
+        graphs.append(capture(k, warmup, steps))
+        longs.append(capture(k, warmup, LONG * steps) if SLOPES else None)
     torch.cuda.synchronize()
     for g in graphs:
         g.replay()
@@ -742,45 +795,39 @@ def time_graphs(kernels, steps: int, warmup: int, rounds: int = 1) -> float:
     for k, t in zip(kernels, times):
         k.step_ms = t[0]
         k.graph_ms = statistics.median(t)
-    del graphs
+    if SLOPES:
+        _, slope = slopes(list(zip(graphs, longs)), steps, max(rounds, 3), stream)
+        for k, t in zip(kernels, slope):
+            k.launch_ms = statistics.median(t)
+    else:
+        for k in kernels:
+            k.launch_ms = k.graph_ms
+    del graphs, longs
     return wall
 
 
 def time_matched(groups, steps: int, rounds: int) -> None:
-    """Each group (a kernel, then its probes) replayed from captured graphs in
-    turn, `rounds` times, one event pair around each replay: a kernel and its
-    probes see the same clocks and memory state, which change from launch to
-    launch (a probe's launches at one size fall into two or three
-    durations). Sets `matched_ms` on each to its median replay's average
-    launch."""
+    """Each group (a kernel, then its probes) timed in turn, `rounds` times,
+    each member's K-launch graph and LONG x K-launch graph back to back
+    (`slopes`): a kernel and its probes see the same clocks and memory
+    state, which change from launch to launch (a probe's launches at one
+    size fall into two or three durations). Sets `matched_ms` on each to its
+    median launch slope and `matched_replay_ms` to its median K-launch span
+    over K."""
     stream = torch.cuda.current_stream()
     here = ctypes.c_void_p(stream.cuda_stream)
     for group in groups:
-        graphs = []
+        pairs = []
         for k in group:
             for i in range(2):
                 k.fire(i, here)
             torch.cuda.synchronize()
-            g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g):
-                captured = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-                for i in range(steps):
-                    k.fire(i, captured)
-            graphs.append(g)
-        for g in graphs:
-            g.replay()
-        torch.cuda.synchronize()
-        events = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in group]
-                  for _ in range(rounds)]
-        for r in range(rounds):
-            for g, (start, end) in zip(graphs, events[r]):
-                start.record(stream)
-                g.replay()
-                end.record(stream)
-        torch.cuda.synchronize()
-        for j, k in enumerate(group):
-            k.matched_ms = statistics.median(events[r][j][0].elapsed_time(events[r][j][1]) for r in range(rounds)) / steps
-        del graphs
+            pairs.append((capture(k, 0, steps), capture(k, 0, LONG * steps) if SLOPES else None))
+        spans, slope = slopes(pairs, steps, rounds, stream)
+        for k, sp, sl in zip(group, spans, slope):
+            k.matched_replay_ms = statistics.median(sp)
+            k.matched_ms = statistics.median(sl) if SLOPES else k.matched_replay_ms
+        del pairs
 
 
 def time_eager(kernels, steps: int) -> None:
@@ -826,10 +873,15 @@ def main():
     ap.add_argument("--only", default="", help="comma-separated kernel names to run (profiling)")
     ap.add_argument("--formats", action="store_true",
                     help="also time every storage type's decode to bf16 (outside the step), reported in 'formats'")
+    ap.add_argument("--no-slopes", action="store_true",
+                    help="no long graphs: per-kernel us is the K-launch replay's span over K (for counter passes: "
+                         "rocprofv3 --pmc has ended in a segmentation fault of its own thread in an 80-launch graph)")
     ap.add_argument("--no-host", action="store_true",
                     help="skip the host cost per call (a child process that launches kernels of its own: profilers "
                          "tracing this process would trace it too)")
     args = ap.parse_args()
+    global SLOPES
+    SLOPES = not args.no_slopes
     if args.gpus != 1:
         print(f"bench.py: this path runs on one GPU; --gpus {args.gpus} is not supported "
               f"(rows shard across GPUs with no exchange, so N GPUs do N times the work)", file=sys.stderr)
@@ -875,17 +927,18 @@ def main():
     for k in kernels:
         if k.name not in probes:
             continue
-        best = min(probes[k.name], key=lambda p: p.graph_ms)
+        best = min(probes[k.name], key=lambda p: p.launch_ms)
         k.ceiling = best
-        gbs = best.bytes / (best.graph_ms * 1e-3) / 1e9
+        gbs = best.bytes / (best.launch_ms * 1e-3) / 1e9
         ceilings[k.name] = {"read_bytes": best.read_bytes, "write_bytes": best.bytes - best.read_bytes,
-                            "probe": best.shape, "chunks_a_lane": best.per_lane, "us": round(best.graph_ms * 1e3, 2),
+                            "probe": best.shape, "chunks_a_lane": best.per_lane, "us": round(best.launch_ms * 1e3, 2),
+                            "us_replay": round(best.graph_ms * 1e3, 2),
                             "GB_s": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
-                            "us_by_probe": {f"{p.shape} {p.per_lane} a lane": round(p.graph_ms * 1e3, 2)
+                            "us_by_probe": {f"{p.shape} {p.per_lane} a lane": round(p.launch_ms * 1e3, 2)
                                             for p in probes[k.name]}}
     # each kernel against its best probe (and the gather against its best row
     # probe) under the same conditions, in alternation
-    best_rows = {name: min(group, key=lambda p: p.graph_ms) for name, group in rows_probes.items()}
+    best_rows = {name: min(group, key=lambda p: p.launch_ms) for name, group in rows_probes.items()}
     groups = [[k, k.ceiling] + ([best_rows[k.name]] if k.name in best_rows else []) for k in kernels
               if k.ceiling is not None]
     time_matched(groups, args.steps, MATCHED_ROUNDS)
@@ -893,24 +946,27 @@ def main():
         k, probe = group[0], group[1]
         matched = {"rounds": MATCHED_ROUNDS, "us": round(k.matched_ms * 1e3, 2),
                    "probe_us": round(probe.matched_ms * 1e3, 2),
-                   "frac_of_probe": round(probe.matched_ms / k.matched_ms, 4)}
+                   "frac_of_probe": round(probe.matched_ms / k.matched_ms, 4),
+                   "us_replay": round(k.matched_replay_ms * 1e3, 2),
+                   "probe_us_replay": round(probe.matched_replay_ms * 1e3, 2)}
         if len(group) > 2:
             matched["row_probe_us"] = round(group[2].matched_ms * 1e3, 2)
             matched["frac_of_row_probe"] = round(group[2].matched_ms / k.matched_ms, 4)
         ceilings[k.name]["matched"] = matched
     for name, group in rows_probes.items():
         p = best_rows[name]
-        gbs = p.bytes / (p.graph_ms * 1e-3) / 1e9
-        ceilings[name]["row_probe"] = {"us": round(p.graph_ms * 1e3, 2), "GB_s": round(gbs, 1),
+        gbs = p.bytes / (p.launch_ms * 1e-3) / 1e9
+        ceilings[name]["row_probe"] = {"us": round(p.launch_ms * 1e3, 2), "GB_s": round(gbs, 1),
                                        "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "what": p.config,
                                        "us_by_shape": {("block per id" if q.slices == 0 else f"{q.slices} waves per id"):
-                                                       round(q.graph_ms * 1e3, 2) for q in group}}
+                                                       round(q.launch_ms * 1e3, 2) for q in group}}
     for r in reads:
-        gbs = r.bytes / (r.graph_ms * 1e-3) / 1e9
-        ceilings[r.name] = {"bytes": r.bytes, "us": round(r.graph_ms * 1e3, 2), "GB_s": round(gbs, 1),
+        gbs = r.bytes / (r.launch_ms * 1e-3) / 1e9
+        ceilings[r.name] = {"bytes": r.bytes, "us": round(r.launch_ms * 1e3, 2), "GB_s": round(gbs, 1),
                             "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "what": r.config}
     for f in floors:
-        ceilings[f.name] = {"us": round(f.graph_ms * 1e3, 2), "what": f.config}
+        ceilings[f.name] = {"us": round(f.launch_ms * 1e3, 2), "us_replay": round(f.graph_ms * 1e3, 2),
+                            "what": f.config}
     for group in probes.values():
         for p in group:
             p.buffers = None
@@ -949,10 +1005,11 @@ def main():
     ms_per_step = wall * 1e3 / args.steps
     table = {}
     for k in kernels:
-        avg = k.graph_ms
+        avg = k.launch_ms
         gbs = k.bytes / (avg * 1e-3) / 1e9
         table[k.name] = {
-            "config": k.config, "us": round(avg * 1e3, 2), "us_step": round(k.step_ms * 1e3, 2),
+            "config": k.config, "us": round(avg * 1e3, 2), "us_replay": round(k.graph_ms * 1e3, 2),
+            "us_step": round(k.step_ms * 1e3, 2),
             "us_eager": round(k.eager_ms * 1e3, 2), "bytes": k.bytes,
             "GB_s": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
             "rows_per_s": round(k.rows / (avg * 1e-3), 1),
@@ -963,7 +1020,7 @@ def main():
             if "row_probe" in ceilings[k.name]:
                 table[k.name]["frac_of_row_probe"] = round(gbs / ceilings[k.name]["row_probe"]["GB_s"], 4)
     # the roofline kernel's launches as the timed step replayed them
-    dominant = max(kernels, key=lambda k: k.graph_ms)
+    dominant = max(kernels, key=lambda k: k.launch_ms)
     dom_avg = dominant.step_ms
     achieved = dominant.bytes / (dom_avg * 1e-3) / 1e9
     # HBM bytes per launch are not measured in this run (counters need a
@@ -997,7 +1054,10 @@ def main():
                         "weights decoded to bf16 (Q4_K [14336,4096]; ConvRot int8 and 4-bit [13824,5120])",
             "step_bytes": step_bytes,
             "parallelism": "single GPU",
-            "timing": "each kernel's launches replayed from a captured HIP graph, one event pair per kernel",
+            "timing": "each kernel's K launches replayed from a captured HIP graph, one event pair per kernel "
+                      "(the timed step, value); per-kernel us: " + (
+                          "the launch slope between K- and 4K-launch graphs" if SLOPES else
+                          "the K-launch replay's span over K (--no-slopes)"),
         },
         "kernels": table,
         "ceilings": ceilings,
