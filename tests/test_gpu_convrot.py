@@ -134,6 +134,34 @@ def test_nan_relative_scales_and_codebooks(hip, group_size):
     same_bits(r.dequantize_bf16(), host_bits(out), "non-finite codebook")
 
 
+@pytest.mark.parametrize("four_bit,group_size", [(False, 0), (True, 32), (True, 64)])
+def test_tiny_row_scales(hip, four_bit, group_size):
+    # Row scales down to the float's smallest steps, where the rotation's
+    # halves round: a wave holding such a row takes the two roundings, the
+    # rest the fma form. Rows of 1,024 columns, four to a wave: rows 0-23
+    # tiny, 24 at the boundary 2^-122 and 25 zero (a wave of the fma form),
+    # 47 tiny in a wave of ordinary rows. The fma form would differ from
+    # the oracle here (3 to 5 rows' BF16 values in each case, checked on the
+    # CPU).
+    rows, cols = 48, 1024
+    rng = np.random.default_rng(95)
+    r = o.random_rotated(rows, cols, rng, four_bit, group_size or 32)
+    tiny = rows // 2
+    r.scales[:tiny] = (rng.uniform(1, 2, tiny) * 2.0 ** rng.integers(-149, -118, tiny)).astype(np.float32)
+    r.scales[tiny] = 2.0 ** -122
+    r.scales[tiny + 1] = 0.0
+    r.scales[-1] = 1e-40
+    table = device_table(hip, r)
+    step(f"rotated dequantize {'4-bit' if four_bit else 'int8'} with tiny row scales")
+    out = torch.empty((rows, cols), dtype=torch.bfloat16, device=DEV)
+    hip.dequantize(table, out)
+    same_bits(r.dequantize_bf16(), host_bits(out), "tiny scales")
+    ids = rng.integers(0, rows, 64).astype(np.int32)
+    got = torch.empty((64, cols), dtype=torch.float32, device=DEV)
+    hip.embedding(table, dev_i32(ids), got)
+    same_bits(r.embedding(ids).view(np.uint32), host_f32(got).view(np.uint32), "tiny scales embedding")
+
+
 def test_ids_outside_the_weight_give_zero_rows(hip):
     rows, cols = 5, 512
     r = o.random_rotated(rows, cols, np.random.default_rng(71), True, 32)
