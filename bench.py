@@ -29,14 +29,15 @@ cost of one call of each entry point (drift_amd/host/launch_cost).
 
 Printed: one JSON line. `value` is the step's algorithmic bytes (the reads
 and writes of the tensors each op names) over the step's wall time;
-`kernels` has each kernel's HIP-event times: `us`, its launch inside a
-graph, the slope between a replay of its K-launch graph and one of 4 K
-launches right after it (median of five such pairs), which leaves out the
-fixed start every replay pays before its first launch (about 18 us on
-MI355X, the same for every graph, so 0.9 us a launch at K = 20); `us_step`,
-its K-launch replay's span over K in the timed step, that start included;
-`us_replay`, the same over five replays. Then GB/s (from `us`), fraction of
-the 8 TB/s HBM peak, fraction of its ceiling and rows/s;
+`kernels` has each kernel's HIP-event times: `us_step`, its K-launch
+replay's span over K in the timed step; `us_replay`, the median over five
+replays; and `us`, the launch inside a graph: `us_replay` less the fixed
+start every replay pays between the event before it and its first launch
+(`graph_start_us`, measured in the run with a one-block launch in graphs
+of K and 4 K launches: about 12 us, 0.6 us a launch at K = 20; the kernel
+trace shows the same gap before every kernel's graph). Then GB/s (from
+`us`), fraction of the 8 TB/s HBM peak, fraction of its ceiling and
+rows/s;
 `ceilings` holds, for each long kernel, the fastest probe moving its bytes
 in its read:write mix with nothing else (drift_stream_mix: blocks that only
 read or only write; drift_wave_copy: one-wave blocks each reading its share
@@ -51,8 +52,8 @@ per-launch floor of a graph replay (`launch_floor`: one block writing one
 launches fall into two or three durations by clock and memory state, so
 each kernel is also replayed in alternation with its best probe
 (`ceilings[k]["matched"]`, and `frac_of_probe_matched`: the ratio of their
-median launch slopes under the same conditions); every probe's `us` is its
-launch slope too;
+median replays under the same conditions, the start taken out of both);
+every probe's `us` is taken the same way;
 `roofline` is the dominant kernel's; `cpu_baseline` is the CPU reference
 arithmetic (the oracle) timed on a bounded sample of the same work on this
 host's cores, scaled to the whole step. With `--formats`, `formats` holds
@@ -87,8 +88,9 @@ from drift_amd import ops as d  # noqa: E402
 HBM_PEAK_GBS = 8000.0
 MATCHED_ROUNDS = 7  # alternations of each kernel with its probe
 GRAPH_ROUNDS = 5  # replays of each kernel's graph: the first is the timed step
-LONG = 4  # the long graph beside each K-launch graph holds LONG x K launches
-SLOPES = True  # False (--no-slopes): no long graphs; `us` is then the K-launch replay's span over K
+LONG = 4  # the graph start's long graph holds LONG x K launches
+START_MS = 0.0  # a graph replay's fixed start (graph_start); 0 with --no-graph-start
+STEPS = 20  # launches a graph holds (--steps)
 MALL_BYTES = 512 << 20
 DEV = "cuda:0"
 
@@ -107,11 +109,9 @@ class Kernel:
         self.launch = launch
         self.cpu = None  # (sample description, seconds for the sample, fraction of a call the sample is)
         self.cpu_all = None  # (threads, seconds for the same sample split across them)
-        self.launch_ms = None  # a launch inside a graph: the slope between K- and LONG x K-launch replays (median)
         self.graph_ms = None  # a K-launch replay's span over K, its fixed start included (median over the rounds)
         self.step_ms = None  # the same in the timed step's replay
-        self.matched_ms = None  # the slope, in alternation with its probe (median round)
-        self.matched_replay_ms = None  # the K-launch replay's span over K in the same rounds (median)
+        self.matched_ms = None  # the same, in alternation with its probe (median replay)
         self.eager_ms = None  # average launch, each made from Python through ctypes
         self.ceiling = None  # the stream probe at this kernel's bytes and read/write mix
 
@@ -126,6 +126,16 @@ class Kernel:
                 raise RuntimeError(f"{self.name}: the launch made no C-ABI call")
             entry, args = ops.kept
             self.calls.append((entry, getattr(lib, entry), args))
+
+    @property
+    def launch_ms(self) -> float:
+        """Average launch inside the graph: the median replay's span over K
+        with the replay's fixed start (START_MS) taken out."""
+        return self.graph_ms - START_MS / STEPS
+
+    @property
+    def matched_launch_ms(self) -> float:
+        return self.matched_ms - START_MS / STEPS
 
     def fire(self, i: int, stream) -> None:
         entry, fn, args = self.calls[i % len(self.calls)]
@@ -421,15 +431,16 @@ def time_formats(hip: d.HipOps, lib, steps: int, warmup: int) -> dict:
     time_graphs(kernels, steps, warmup)
     time_graphs([p for group in probes.values() for p in group], steps, warmup)
     for k in kernels:
-        k.ceiling = min(probes[k.name], key=lambda p: p.launch_ms)
+        k.ceiling = min(probes[k.name], key=lambda p: p.graph_ms)
     time_matched([[k, k.ceiling] for k in kernels], steps, MATCHED_ROUNDS)
     out = {}
     for k in kernels:
         gbs = k.bytes / (k.launch_ms * 1e-3) / 1e9
         out[k.name] = {"config": k.config, "us": round(k.launch_ms * 1e3, 2),
                        "us_replay": round(k.graph_ms * 1e3, 2), "bytes": k.bytes, "GB_s": round(gbs, 1),
-                       "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "probe_us": round(k.ceiling.matched_ms * 1e3, 2),
-                       "frac_of_probe_matched": round(k.ceiling.matched_ms / k.matched_ms, 4)}
+                       "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+                       "probe_us": round(k.ceiling.matched_launch_ms * 1e3, 2),
+                       "frac_of_probe_matched": round(k.ceiling.matched_launch_ms / k.matched_launch_ms, 4)}
     for k in kernels:
         k.calls = []
     for group in probes.values():
@@ -720,60 +731,62 @@ def capture(k: Kernel, first: int, launches: int):
     return g
 
 
-def slopes(pairs, steps: int, rounds: int, stream):
-    """For each (K-launch graph, LONG x K-launch graph), `rounds` times in
-    turn: the two replayed back to back, an event before, between and after.
-    Returns, per pair, each round's K-launch span over K and its launch
-    slope, (long span - K span) / ((LONG - 1) K): a replay's fixed start
-    (the span from the event before it to its first launch, the same for
-    every graph, about 18 us here) cancels, and the slope is the launch's
-    own time inside a graph, the figure a kernel trace's average duration
-    gives."""
-    spans = [[] for _ in pairs]
-    slope = [[] for _ in pairs]
-    for g, long in pairs:  # a first replay of each, untimed
-        g.replay()
-        if long is not None:
-            long.replay()
+def graph_start(floor: Kernel, steps: int, rounds: int = 7) -> float:
+    """The fixed start every graph replay pays between the event before it
+    and its first launch, in ms: `floor`'s launch (one block writing 16
+    bytes) in a graph of `steps` launches and in one of LONG x `steps`,
+    replayed back to back after an untimed replay, `rounds` times. A launch
+    of it costs the same at every position of a graph, so each round's
+    start is (LONG t_K - t_long) / (LONG - 1); the median is returned. The
+    kernel trace shows the same gap before every kernel's graph (17.5-18 us
+    between one graph's last kernel and the next graph's first, the event's
+    own share included), so it is subtracted from every kernel's replay."""
+    stream = torch.cuda.current_stream()
+    here = ctypes.c_void_p(stream.cuda_stream)
+    for i in range(2):
+        floor.fire(i, here)
     torch.cuda.synchronize()
+    short, long = capture(floor, 0, steps), capture(floor, 0, LONG * steps)
+    short.replay()
+    long.replay()
+    torch.cuda.synchronize()
+    starts = []
     for _ in range(rounds):
-        events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in pairs]
-        for (g, long), (a, b, c) in zip(pairs, events):
-            a.record(stream)
-            g.replay()
-            b.record(stream)
-            if long is not None:
-                long.replay()
-            c.record(stream)
+        a, b, c = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+        short.replay()
+        a.record(stream)
+        short.replay()
+        b.record(stream)
+        long.replay()
+        c.record(stream)
         torch.cuda.synchronize()
-        for j, ((_, long), (a, b, c)) in enumerate(zip(pairs, events)):
-            short_ms = a.elapsed_time(b)
-            spans[j].append(short_ms / steps)
-            if long is not None:
-                slope[j].append((b.elapsed_time(c) - short_ms) / ((LONG - 1) * steps))
-    return spans, slope
+        starts.append((LONG * a.elapsed_time(b) - b.elapsed_time(c)) / (LONG - 1))
+    del short, long
+    return max(statistics.median(starts), 0.0)
 
 
 def time_graphs(kernels, steps: int, warmup: int, rounds: int = 1) -> float:
     """Each kernel's `steps` launches captured in a HIP graph (rotating its
     buffer sets), replayed with one event pair around the replay on the
-    replaying stream. The first round of replays (every kernel once, in
+    replaying stream: the average launch is the span over `steps`, with no
+    host call in it. The first round of replays (every kernel once, in
     order) is the timed region: its wall time is returned and each kernel's
-    span over `steps` in it kept as `step_ms`. Further rounds, after it,
-    replay the same graphs in the same order; `graph_ms` is each kernel's
-    median span over `steps` over all rounds. Then `launch_ms`: the median
-    launch slope of each kernel's graph and a graph of LONG x `steps` of its
-    launches, replayed back to back (`slopes`), which leaves out the fixed
-    start that every replay's span carries."""
+    figure in it kept as `step_ms`. Further rounds, after it, replay the same
+    graphs in the same order; `graph_ms` is each kernel's median over all
+    rounds, so one slow replay does not stand for the kernel."""
     stream = torch.cuda.current_stream()
     here = ctypes.c_void_p(stream.cuda_stream)
-    graphs, longs = [], []
+    graphs = []
     for k in kernels:
         for i in range(warmup):
             k.fire(i, here)
         torch.cuda.synchronize()
-        graphs.append(capture(k, warmup, steps))
-        longs.append(capture(k, warmup, LONG * steps) if SLOPES else None)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            captured = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+            for i in range(steps):
+                k.fire(warmup + i, captured)
+        graphs.append(g)
     torch.cuda.synchronize()
     for g in graphs:
         g.replay()
@@ -795,39 +808,45 @@ def time_graphs(kernels, steps: int, warmup: int, rounds: int = 1) -> float:
     for k, t in zip(kernels, times):
         k.step_ms = t[0]
         k.graph_ms = statistics.median(t)
-    if SLOPES:
-        _, slope = slopes(list(zip(graphs, longs)), steps, max(rounds, 3), stream)
-        for k, t in zip(kernels, slope):
-            k.launch_ms = statistics.median(t)
-    else:
-        for k in kernels:
-            k.launch_ms = k.graph_ms
-    del graphs, longs
+    del graphs
     return wall
 
 
 def time_matched(groups, steps: int, rounds: int) -> None:
-    """Each group (a kernel, then its probes) timed in turn, `rounds` times,
-    each member's K-launch graph and LONG x K-launch graph back to back
-    (`slopes`): a kernel and its probes see the same clocks and memory
-    state, which change from launch to launch (a probe's launches at one
-    size fall into two or three durations). Sets `matched_ms` on each to its
-    median launch slope and `matched_replay_ms` to its median K-launch span
-    over K."""
+    """Each group (a kernel, then its probes) replayed from captured graphs in
+    turn, `rounds` times, one event pair around each replay: a kernel and its
+    probes see the same clocks and memory state, which change from launch to
+    launch (a probe's launches at one size fall into two or three
+    durations). Sets `matched_ms` on each to its median replay's average
+    launch."""
     stream = torch.cuda.current_stream()
     here = ctypes.c_void_p(stream.cuda_stream)
     for group in groups:
-        pairs = []
+        graphs = []
         for k in group:
             for i in range(2):
                 k.fire(i, here)
             torch.cuda.synchronize()
-            pairs.append((capture(k, 0, steps), capture(k, 0, LONG * steps) if SLOPES else None))
-        spans, slope = slopes(pairs, steps, rounds, stream)
-        for k, sp, sl in zip(group, spans, slope):
-            k.matched_replay_ms = statistics.median(sp)
-            k.matched_ms = statistics.median(sl) if SLOPES else k.matched_replay_ms
-        del pairs
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                captured = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+                for i in range(steps):
+                    k.fire(i, captured)
+            graphs.append(g)
+        for g in graphs:
+            g.replay()
+        torch.cuda.synchronize()
+        events = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in group]
+                  for _ in range(rounds)]
+        for r in range(rounds):
+            for g, (start, end) in zip(graphs, events[r]):
+                start.record(stream)
+                g.replay()
+                end.record(stream)
+        torch.cuda.synchronize()
+        for j, k in enumerate(group):
+            k.matched_ms = statistics.median(events[r][j][0].elapsed_time(events[r][j][1]) for r in range(rounds)) / steps
+        del graphs
 
 
 def time_eager(kernels, steps: int) -> None:
@@ -873,15 +892,16 @@ def main():
     ap.add_argument("--only", default="", help="comma-separated kernel names to run (profiling)")
     ap.add_argument("--formats", action="store_true",
                     help="also time every storage type's decode to bf16 (outside the step), reported in 'formats'")
-    ap.add_argument("--no-slopes", action="store_true",
-                    help="no long graphs: per-kernel us is the K-launch replay's span over K (for counter passes: "
-                         "rocprofv3 --pmc has ended in a segmentation fault of its own thread in an 80-launch graph)")
+    ap.add_argument("--no-graph-start", action="store_true",
+                    help="no long graph: the graph start is not measured, per-kernel us is the K-launch replay's span "
+                         "over K (for counter passes: rocprofv3 --pmc has ended in a segmentation fault of its own "
+                         "thread in an 80-launch graph)")
     ap.add_argument("--no-host", action="store_true",
                     help="skip the host cost per call (a child process that launches kernels of its own: profilers "
                          "tracing this process would trace it too)")
     args = ap.parse_args()
-    global SLOPES
-    SLOPES = not args.no_slopes
+    global START_MS, STEPS
+    STEPS = args.steps
     if args.gpus != 1:
         print(f"bench.py: this path runs on one GPU; --gpus {args.gpus} is not supported "
               f"(rows shard across GPUs with no exchange, so N GPUs do N times the work)", file=sys.stderr)
@@ -921,13 +941,17 @@ def main():
     largest_first = sorted(kernels, key=lambda k: k.bytes, reverse=True)
     wall = time_graphs(largest_first, args.steps, args.warmup, rounds=GRAPH_ROUNDS)
     time_eager(largest_first, args.steps)
+    # the fixed start of a graph replay, which every kernel's and probe's
+    # replay span carries (taken out of each `us`)
+    if not args.no_graph_start:
+        START_MS = graph_start(floor_probe(lib), args.steps)
     time_graphs([p for group in probes.values() for p in group] + [p for group in rows_probes.values() for p in group]
                 + reads + floors, args.steps, args.warmup)
     ceilings = {}
     for k in kernels:
         if k.name not in probes:
             continue
-        best = min(probes[k.name], key=lambda p: p.launch_ms)
+        best = min(probes[k.name], key=lambda p: p.graph_ms)
         k.ceiling = best
         gbs = best.bytes / (best.launch_ms * 1e-3) / 1e9
         ceilings[k.name] = {"read_bytes": best.read_bytes, "write_bytes": best.bytes - best.read_bytes,
@@ -938,20 +962,20 @@ def main():
                                             for p in probes[k.name]}}
     # each kernel against its best probe (and the gather against its best row
     # probe) under the same conditions, in alternation
-    best_rows = {name: min(group, key=lambda p: p.launch_ms) for name, group in rows_probes.items()}
+    best_rows = {name: min(group, key=lambda p: p.graph_ms) for name, group in rows_probes.items()}
     groups = [[k, k.ceiling] + ([best_rows[k.name]] if k.name in best_rows else []) for k in kernels
               if k.ceiling is not None]
     time_matched(groups, args.steps, MATCHED_ROUNDS)
     for group in groups:
         k, probe = group[0], group[1]
-        matched = {"rounds": MATCHED_ROUNDS, "us": round(k.matched_ms * 1e3, 2),
-                   "probe_us": round(probe.matched_ms * 1e3, 2),
-                   "frac_of_probe": round(probe.matched_ms / k.matched_ms, 4),
-                   "us_replay": round(k.matched_replay_ms * 1e3, 2),
-                   "probe_us_replay": round(probe.matched_replay_ms * 1e3, 2)}
+        matched = {"rounds": MATCHED_ROUNDS, "us": round(k.matched_launch_ms * 1e3, 2),
+                   "probe_us": round(probe.matched_launch_ms * 1e3, 2),
+                   "frac_of_probe": round(probe.matched_launch_ms / k.matched_launch_ms, 4),
+                   "us_replay": round(k.matched_ms * 1e3, 2),
+                   "probe_us_replay": round(probe.matched_ms * 1e3, 2)}
         if len(group) > 2:
-            matched["row_probe_us"] = round(group[2].matched_ms * 1e3, 2)
-            matched["frac_of_row_probe"] = round(group[2].matched_ms / k.matched_ms, 4)
+            matched["row_probe_us"] = round(group[2].matched_launch_ms * 1e3, 2)
+            matched["frac_of_row_probe"] = round(group[2].matched_launch_ms / k.matched_launch_ms, 4)
         ceilings[k.name]["matched"] = matched
     for name, group in rows_probes.items():
         p = best_rows[name]
@@ -1020,7 +1044,7 @@ def main():
             if "row_probe" in ceilings[k.name]:
                 table[k.name]["frac_of_row_probe"] = round(gbs / ceilings[k.name]["row_probe"]["GB_s"], 4)
     # the roofline kernel's launches as the timed step replayed them
-    dominant = max(kernels, key=lambda k: k.launch_ms)
+    dominant = max(kernels, key=lambda k: k.graph_ms)
     dom_avg = dominant.step_ms
     achieved = dominant.bytes / (dom_avg * 1e-3) / 1e9
     # HBM bytes per launch are not measured in this run (counters need a
@@ -1055,10 +1079,12 @@ def main():
             "step_bytes": step_bytes,
             "parallelism": "single GPU",
             "timing": "each kernel's K launches replayed from a captured HIP graph, one event pair per kernel "
-                      "(the timed step, value); per-kernel us: " + (
-                          "the launch slope between K- and 4K-launch graphs" if SLOPES else
-                          "the K-launch replay's span over K (--no-slopes)"),
+                      "(the timed step, value); per-kernel us: the median replay's span over K less graph_start_us / K",
         },
+        "graph_start_us": {"us": round(START_MS * 1e3, 2),
+                           "what": "the fixed start of a graph replay, between the event before it and its first "
+                                   "launch: a one-block launch in graphs of K and 4K launches, median of 7 pairs; "
+                                   "each kernel's and probe's us is its K-launch replay's span less this, over K"},
         "kernels": table,
         "ceilings": ceilings,
         "formats": formats,
