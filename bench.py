@@ -739,8 +739,8 @@ def graph_start(floor: Kernel, steps: int, rounds: int = 7) -> float:
     of it costs the same at every position of a graph, so each round's
     start is (LONG t_K - t_long) / (LONG - 1); the median is returned. The
     kernel trace shows the same gap before every kernel's graph (17.5-18 us
-    between one graph's last kernel and the next graph's first, the event's
-    own share included), so it is subtracted from every kernel's replay."""
+    from one graph's last kernel to the next graph's first, whatever the
+    kernels), so one start is subtracted from every kernel's replay."""
     stream = torch.cuda.current_stream()
     here = ctypes.c_void_p(stream.cuda_stream)
     for i in range(2):
