@@ -30,8 +30,7 @@ namespace {
 // with chunk i + half/N; interleaved: one chunk, its N/2 pairs inside. Tail
 // chunks (from rotary on) are copied.
 template <typename T>
-__device__ __forceinline__ void turn_chunks(const T* xh, T* oh, int item, int dim, int rotary, int layout,
-                                            const double2* cs) {
+__device__ __forceinline__ void turn_chunks(const T* xh, T* oh, int item, int rotary, int layout, const double2* cs) {
   constexpr int N = Chunk<T>::N;
   const int half = rotary / 2;
   if (layout == DRIFT_ROPE_NEOX) {
@@ -88,7 +87,7 @@ __global__ void __launch_bounds__(256) rope_kernel(const T* x, const int32_t* po
       const T* xh = xt + (int64_t)h * p.dim;
       T* oh = ot + (int64_t)h * p.dim;
       if constexpr (CHUNKED)
-        turn_chunks<T>(xh, oh, j, p.dim, p.rotary, p.layout, cs);
+        turn_chunks<T>(xh, oh, j, p.rotary, p.layout, cs);
       else
         turn_slot<T>(j, p.dim, p.rotary, p.layout, cs, [&](int d) { return (double)load_one(xh + d); }, oh);
     }
@@ -162,7 +161,7 @@ __global__ void __launch_bounds__(256) rope_3d_kernel(const T* x, T* out, Rope3d
       const T* xh = xt + (int64_t)h * p.dim;
       T* oh = ot + (int64_t)h * p.dim;
       if constexpr (CHUNKED)
-        turn_chunks<T>(xh, oh, j, p.dim, p.dim, DRIFT_ROPE_INTERLEAVED, cs);
+        turn_chunks<T>(xh, oh, j, p.dim, DRIFT_ROPE_INTERLEAVED, cs);
       else
         turn_slot<T>(j, p.dim, p.dim, DRIFT_ROPE_INTERLEAVED, cs, [&](int d) { return (double)load_one(xh + d); },
                      oh);
