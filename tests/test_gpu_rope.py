@@ -135,9 +135,13 @@ def test_rope_table(hip, halves, per_head, shape, pairs):
     assert_bf16(o.to_bf16(o.rope_table(o.from_bf16(xb), cos, sin, halves)), host_bits(outb), what="ropeTable bf16")
 
 
+# tokens of 1 to 18 chunks a lane (bf16: 1 to 72 heads of 128), each
+# wave-per-token variant, and heads of 126 (not whole chunks)
 @pytest.mark.parametrize("grid,heads,dim,samples", [((3, 4, 5), 2, 128, 2), ((1, 1, 9), 3, 128, 1),
                                                     ((2, 3, 7), 4, 64, 3), ((2, 2, 3), 2, 126, 1),
-                                                    ((1, 1, 1), 1, 128, 2)])
+                                                    ((1, 1, 1), 1, 128, 2), ((2, 3, 5), 4, 128, 2),
+                                                    ((3, 2, 2), 16, 128, 1), ((1, 2, 3), 64, 128, 1),
+                                                    ((1, 2, 2), 72, 128, 1)])
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 def test_rope_3d(hip, grid, heads, dim, samples, dtype):
     frames, rows, cols = grid
